@@ -1,0 +1,404 @@
+// C-ABI of libbs_hip.so: index residency, search dispatch, primitive entry points.
+// Declarations and reference citations: include/bs_hip.h.
+#include "bs_hip.h"
+#include "bs_launch.hpp"
+
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <vector>
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const std::string& msg) {
+    g_err = msg;
+    return code;
+}
+
+#define HIP_TRY(call)                                                                          \
+    do {                                                                                       \
+        hipError_t e_ = (call);                                                                \
+        if (e_ != hipSuccess)                                                                  \
+            return fail(BS_EHIP, std::string(#call) + " failed: " + hipGetErrorString(e_));  \
+    } while (0)
+
+uint32_t log2_ceil(uint32_t v) {
+    uint32_t b = 0;
+    while ((1ull << b) < v) ++b;
+    return b;
+}
+
+bsd::L2Shape l2_shape(uint32_t dim) {
+    bsd::L2Shape L;
+    L.chunks = (dim + 3) / 4;
+    L.G = 1;
+    while (L.G < L.chunks && L.G < 64) L.G <<= 1;
+    L.gshift = log2_ceil(L.G);
+    L.QR = (L.chunks + L.G - 1) / L.G;
+    L.rpp = 64 / L.G;
+    return L;
+}
+
+int check_device() {
+    int dev = 0;
+    HIP_TRY(hipGetDevice(&dev));
+    hipDeviceProp_t prop;
+    HIP_TRY(hipGetDeviceProperties(&prop, dev));
+    if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+        return fail(BS_ENODEV, std::string("libbs_hip.so is built for gfx950 (MI355X); device is ") + prop.gcnArchName);
+    if (prop.warpSize != 64) return fail(BS_ENODEV, "wavefront size 64 required");
+    return BS_OK;
+}
+
+}  // namespace
+
+struct bs_index_s {
+    int device = 0;
+    uint64_t n = 0;
+    uint32_t dim = 0, dstride = 0, degree = 0;
+    float* d_vecs = nullptr;
+    uint32_t* d_edges = nullptr;
+    // rabitq node records: [vec dstride | ids R | tx R | fdq R | fvq R | codes R*wpp],
+    // rounded up to 32 words (128 B)
+    uint32_t pdim = 0, wpp = 0, rec_words = 0, rec_ids = 0, rec_fac = 0, rec_codes = 0;
+    uint32_t* d_recs = nullptr;
+    float* d_signs = nullptr;
+    size_t max_lds = 65536;
+};
+
+extern "C" const char* bs_last_error(void) { return g_err.c_str(); }
+
+// helpers for the primitive entry points (bs_debug.hip)
+int bs_internal_vecs(bs_index ix, const float** vecs, uint32_t* dstride) {
+    *vecs = ix->d_vecs;
+    *dstride = ix->dstride;
+    return BS_OK;
+}
+void bs_internal_set_error(const std::string& msg) { g_err = msg; }
+
+extern "C" int bs_index_create(const float* vecs, const uint32_t* edges, uint64_t n, uint32_t dim,
+                               uint32_t degree, bs_index* out) {
+    if (!out) return fail(BS_EINVAL, "out is null");
+    *out = nullptr;
+    if (!vecs || !edges) return fail(BS_EINVAL, "vecs and edges must be given");
+    if (n == 0 || n > 0x7FFFFFFFull) return fail(BS_EINVAL, "need 0 < n < 2^31");
+    if (dim == 0 || dim > 1024) return fail(BS_EINVAL, "dim must be in 1..1024");
+    if (degree == 0 || degree > 128) return fail(BS_EINVAL, "degree must be in 1..128");
+    // every neighbour id must address a node (the kernels gather rows without bounds checks)
+    for (uint64_t i = 0, cnt = n * degree; i < cnt; ++i) {
+        const uint32_t e = edges[i];
+        if (e != 0xFFFFFFFFu && e >= n)
+            return fail(BS_EINVAL, "edge " + std::to_string(i) + " points to node " + std::to_string(e) +
+                                       " >= n = " + std::to_string(n));
+    }
+    int rc = check_device();
+    if (rc) return rc;
+    int device = 0;
+    HIP_TRY(hipGetDevice(&device));
+    bs_index_s* ix = new bs_index_s();
+    ix->n = n;
+    ix->dim = dim;
+    ix->dstride = (dim + 3) & ~3u;
+    ix->degree = degree;
+    ix->device = device;
+    int lds = 0;
+    if (hipDeviceGetAttribute(&lds, hipDeviceAttributeMaxSharedMemoryPerBlock, ix->device) == hipSuccess && lds > 0)
+        ix->max_lds = static_cast<size_t>(lds);
+    const size_t vbytes = n * ix->dstride * sizeof(float);
+    if (hipMalloc(&ix->d_vecs, vbytes) != hipSuccess) {
+        delete ix;
+        return fail(BS_ENOMEM, "hipMalloc of the vectors failed");
+    }
+    if (hipMalloc(&ix->d_edges, n * degree * sizeof(uint32_t)) != hipSuccess) {
+        (void)hipFree(ix->d_vecs);
+        delete ix;
+        return fail(BS_ENOMEM, "hipMalloc of the edges failed");
+    }
+    hipError_t e = hipSuccess;
+    if (ix->dstride == dim) {
+        e = hipMemcpy(ix->d_vecs, vecs, vbytes, hipMemcpyHostToDevice);
+    } else {
+        e = hipMemset(ix->d_vecs, 0, vbytes);
+        if (e == hipSuccess)
+            e = hipMemcpy2D(ix->d_vecs, ix->dstride * sizeof(float), vecs, dim * sizeof(float), dim * sizeof(float),
+                            n, hipMemcpyHostToDevice);
+    }
+    if (e == hipSuccess) e = hipMemcpy(ix->d_edges, edges, n * degree * sizeof(uint32_t), hipMemcpyHostToDevice);
+    if (e != hipSuccess) {
+        bs_index_destroy(ix);
+        return fail(BS_EHIP, std::string("upload failed: ") + hipGetErrorString(e));
+    }
+    *out = ix;
+    return BS_OK;
+}
+
+extern "C" int bs_index_attach_rabitq(bs_index ix, const uint32_t* codes, const float* factors,
+                                      const float* signs, uint32_t padded_dim) {
+    if (!ix || !codes || !factors || !signs) return fail(BS_EINVAL, "null argument");
+    uint32_t p = 1;
+    while (p < ix->dim) p <<= 1;
+    if (padded_dim != p) return fail(BS_EINVAL, "padded_dim must be pow2ceil(dim) = " + std::to_string(p));
+    if (padded_dim < 32 || padded_dim > 2048) return fail(BS_EINVAL, "padded_dim must be in 32..2048");
+    const uint32_t R = ix->degree, wpp = padded_dim / 32;
+    uint32_t rw = ix->dstride + R + 3 * R + R * wpp;
+    rw = (rw + 31) & ~31u;
+    // assemble the records on the host in blocks and upload
+    if (ix->d_recs) {
+        (void)hipFree(ix->d_recs);
+        ix->d_recs = nullptr;
+    }
+    if (ix->d_signs) {
+        (void)hipFree(ix->d_signs);
+        ix->d_signs = nullptr;
+    }
+    if (hipMalloc(&ix->d_recs, ix->n * static_cast<size_t>(rw) * 4) != hipSuccess)
+        return fail(BS_ENOMEM, "hipMalloc of the rabitq records failed");
+    HIP_TRY(hipMalloc(&ix->d_signs, padded_dim * sizeof(float)));
+    HIP_TRY(hipMemcpy(ix->d_signs, signs, padded_dim * sizeof(float), hipMemcpyHostToDevice));
+    ix->pdim = padded_dim;
+    ix->wpp = wpp;
+    ix->rec_words = rw;
+    ix->rec_ids = ix->dstride;
+    ix->rec_fac = ix->rec_ids + R;
+    ix->rec_codes = ix->rec_fac + 3 * R;
+    const uint64_t block = std::max<uint64_t>(1, (64ull << 20) / (4ull * rw));
+    std::vector<uint32_t> host(block * rw);
+    std::vector<float> vtmp(block * ix->dstride);
+    std::vector<uint32_t> etmp(block * R);
+    for (uint64_t r0 = 0; r0 < ix->n; r0 += block) {
+        const uint64_t m = std::min(block, ix->n - r0);
+        HIP_TRY(hipMemcpy(vtmp.data(), ix->d_vecs + r0 * ix->dstride, m * ix->dstride * 4, hipMemcpyDeviceToHost));
+        HIP_TRY(hipMemcpy(etmp.data(), ix->d_edges + r0 * R, m * R * 4, hipMemcpyDeviceToHost));
+        std::fill(host.begin(), host.begin() + m * rw, 0u);
+        for (uint64_t i = 0; i < m; ++i) {
+            uint32_t* rec = host.data() + i * rw;
+            std::memcpy(rec, vtmp.data() + i * ix->dstride, 4ull * ix->dstride);
+            std::memcpy(rec + ix->rec_ids, etmp.data() + i * R, 4ull * R);
+            std::memcpy(rec + ix->rec_fac, factors + (r0 + i) * 3 * R, 12ull * R);
+            std::memcpy(rec + ix->rec_codes, codes + (r0 + i) * R * wpp, 4ull * R * wpp);
+        }
+        HIP_TRY(hipMemcpy(ix->d_recs + r0 * rw, host.data(), m * rw * 4ull, hipMemcpyHostToDevice));
+    }
+    return BS_OK;
+}
+
+extern "C" int bs_index_info(bs_index ix, uint64_t* n, uint32_t* dim, uint32_t* degree,
+                             uint32_t* padded_dim, int* has_rabitq) {
+    if (!ix) return fail(BS_EINVAL, "null index");
+    if (n) *n = ix->n;
+    if (dim) *dim = ix->dim;
+    if (degree) *degree = ix->degree;
+    if (padded_dim) *padded_dim = ix->pdim;
+    if (has_rabitq) *has_rabitq = ix->d_recs != nullptr;
+    return BS_OK;
+}
+
+extern "C" void bs_index_destroy(bs_index ix) {
+    if (!ix) return;
+    if (ix->d_vecs) (void)hipFree(ix->d_vecs);
+    if (ix->d_edges) (void)hipFree(ix->d_edges);
+    if (ix->d_recs) (void)hipFree(ix->d_recs);
+    if (ix->d_signs) (void)hipFree(ix->d_signs);
+    delete ix;
+}
+
+namespace {
+
+struct Plan {
+    bsd::SearchParams p;
+    int TR, CR, QMAX, mode;
+    dim3 grid, block;
+    size_t lds;
+};
+
+// validate the configuration and fill the kernel parameters
+int make_plan(bs_index ix, const bs_search_cfg* cfg, uint64_t nq, Plan& pl) {
+    if (!ix || !cfg) return fail(BS_EINVAL, "null argument");
+    const int mode = cfg->mode;
+    if (mode < BS_BASE || mode > BS_RABITQ) return fail(BS_EINVAL, "unknown mode " + std::to_string(mode));
+    if (mode == BS_RABITQ && !ix->d_recs) return fail(BS_EINVAL, "rabitq mode needs bs_index_attach_rabitq first");
+    const uint32_t T = cfg->topk_size;
+    if (T == 0 || T > 512) return fail(BS_EINVAL, "topk_size must be in 1..512");
+    if (cfg->K == 0) return fail(BS_EINVAL, "K must be >= 1");
+    if (mode != BS_RABITQ && T < cfg->K)
+        return fail(BS_EINVAL, "topk_size (" + std::to_string(T) + ") must be >= K (" + std::to_string(cfg->K) + ")");
+    if (cfg->K > 4096) return fail(BS_EINVAL, "K must be <= 4096");
+    if (cfg->entry_point >= ix->n) return fail(BS_EINVAL, "entry_point out of range");
+    if (cfg->max_iterations < 0) return fail(BS_EINVAL, "max_iterations must be >= 0");
+    if (cfg->reset_interval < 0) return fail(BS_EINVAL, "reset_interval must be >= 0");
+    uint32_t ny = cfg->queries_per_group ? cfg->queries_per_group : 1;
+    if (ny != 1 && ny != 2 && ny != 4 && ny != 8) return fail(BS_EINVAL, "queries_per_group must be 1, 2, 4 or 8");
+    const uint32_t cap = cfg->filter_capacity;
+    if (cap > (1u << 16) && mode != BS_GROUP_BLOOM) return fail(BS_EINVAL, "filter_capacity must be <= 65536");
+    if (cap > (1u << 22)) return fail(BS_EINVAL, "filter_capacity must be <= 2^22");
+
+    pl.mode = mode;
+    pl.TR = T <= 64 ? 1 : T <= 128 ? 2 : T <= 256 ? 4 : 8;
+    pl.CR = ix->degree <= 64 ? 1 : 2;
+    bsd::L2Shape L = l2_shape(ix->dim);
+    pl.QMAX = L.QR <= 1 ? 1 : 4;
+    if (L.QR > 4) return fail(BS_EINVAL, "dim too large");
+
+    bsd::SearchParams& p = pl.p;
+    std::memset(&p, 0, sizeof(p));
+    p.vecs = ix->d_vecs;
+    p.edges = ix->d_edges;
+    p.recs = ix->d_recs;
+    p.signs = ix->d_signs;
+    p.nq = nq;
+    p.dim = ix->dim;
+    p.dstride = ix->dstride;
+    p.R = ix->degree;
+    p.K = cfg->K;
+    p.T = T;
+    p.entry = cfg->entry_point;
+    p.max_it = cfg->max_iterations;
+    p.reset = cfg->reset_interval;
+    p.L = L;
+    uint32_t filter_bytes;
+    if (mode == BS_GROUP_BLOOM) {
+        uint32_t b = log2_ceil(cap);
+        if (b < 5) b = 5;
+        p.filter_bits = b;
+        filter_bytes = (1u << (b - 5)) * 4;
+    } else {
+        p.filter_bits = log2_ceil(cap);
+        filter_bytes = (1u << p.filter_bits) * 4;
+    }
+    uint32_t scratch = 512u * pl.TR;
+    if (mode == BS_RABITQ) {
+        p.pdim = ix->pdim;
+        p.wpp = ix->wpp;
+        p.rec_words = ix->rec_words;
+        p.rec_ids = ix->rec_ids;
+        p.rec_fac = ix->rec_fac;
+        p.rec_codes = ix->rec_codes;
+        scratch = std::max(scratch, 4u * ix->pdim + 24u * ix->wpp);
+    }
+    auto al = [](uint32_t v) { return (v + 15u) & ~15u; };
+    p.off_filter = 0;
+    p.off_scratch = al(filter_bytes);
+    p.off_cand = p.off_scratch + al(scratch);
+    p.lds_wave = al(p.off_cand + 64u * pl.CR * 8u);
+    pl.lds = static_cast<size_t>(p.lds_wave) * ny;
+    if (pl.lds > ix->max_lds)
+        return fail(BS_EINVAL, "LDS per workgroup " + std::to_string(pl.lds) + " B exceeds the device limit " +
+                                   std::to_string(ix->max_lds) + " B (lower filter_capacity or queries_per_group)");
+    pl.block = dim3(64 * ny);
+    const uint64_t groups = (nq + ny - 1) / ny;
+    if (groups > 0x7FFFFFFFull) return fail(BS_EINVAL, "too many queries for one launch");
+    pl.grid = dim3(static_cast<uint32_t>(groups));
+    return BS_OK;
+}
+
+hipError_t launch(const Plan& pl, hipStream_t s) {
+    switch (pl.mode) {
+    case BS_GROUP_BLOOM: return bsd::launch_search_bloom(pl.p, pl.TR, pl.CR, pl.QMAX, pl.grid, pl.block, pl.lds, s);
+    case BS_RABITQ: return bsd::launch_search_rabitq(pl.p, pl.TR, pl.CR, pl.QMAX, pl.grid, pl.block, pl.lds, s);
+    default: return bsd::launch_search_hash(pl.p, pl.TR, pl.CR, pl.QMAX, pl.grid, pl.block, pl.lds, s);
+    }
+}
+
+}  // namespace
+
+extern "C" int bs_search_device(bs_index ix, const bs_search_cfg* cfg, const float* d_queries, uint64_t nq,
+                                uint32_t* d_results, float* d_dists, uint32_t* d_per_query, void* stream,
+                                int sync, bs_stats* stats) {
+    Plan pl;
+    int rc = make_plan(ix, cfg, nq, pl);
+    if (rc) return rc;
+    if (nq == 0) {
+        if (stats) std::memset(stats, 0, sizeof(*stats));
+        return BS_OK;
+    }
+    if (!d_queries || !d_results) return fail(BS_EINVAL, "queries and results must be given");
+    pl.p.queries = d_queries;
+    pl.p.results = d_results;
+    pl.p.dists = d_dists;
+    pl.p.per_query = d_per_query;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    if (sync) {
+        HIP_TRY(hipEventCreate(&e0));
+        HIP_TRY(hipEventCreate(&e1));
+        HIP_TRY(hipEventRecord(e0, s));
+    }
+    hipError_t le = launch(pl, s);
+    if (le != hipSuccess) {
+        if (e0) (void)hipEventDestroy(e0);
+        if (e1) (void)hipEventDestroy(e1);
+        return fail(BS_EHIP, std::string("search launch failed: ") + hipGetErrorString(le));
+    }
+    if (sync) {
+        HIP_TRY(hipEventRecord(e1, s));
+        HIP_TRY(hipEventSynchronize(e1));
+        float ms = 0;
+        HIP_TRY(hipEventElapsedTime(&ms, e0, e1));
+        (void)hipEventDestroy(e0);
+        (void)hipEventDestroy(e1);
+        if (stats) {
+            std::memset(stats, 0, sizeof(*stats));
+            stats->kernel_ms = ms;
+            if (d_per_query) {
+                std::vector<uint32_t> pq(nq * 5);
+                HIP_TRY(hipMemcpy(pq.data(), d_per_query, nq * 5 * 4, hipMemcpyDeviceToHost));
+                for (uint64_t i = 0; i < nq; ++i) {
+                    stats->iterations += pq[i * 5 + 0];
+                    stats->expansions += pq[i * 5 + 1];
+                    stats->dist_evals += pq[i * 5 + 2];
+                    stats->est_evals += pq[i * 5 + 3];
+                    stats->rerank_evals += pq[i * 5 + 4];
+                }
+            }
+        }
+    }
+    return BS_OK;
+}
+
+extern "C" int bs_search(bs_index ix, const bs_search_cfg* cfg, const float* queries, uint64_t nq,
+                         uint32_t* results, float* dists, bs_stats* stats) {
+    Plan pl;
+    int rc = make_plan(ix, cfg, nq, pl);
+    if (rc) return rc;
+    if (nq == 0) {
+        if (stats) std::memset(stats, 0, sizeof(*stats));
+        return BS_OK;
+    }
+    if (!queries || !results) return fail(BS_EINVAL, "queries and results must be given");
+    float* dq = nullptr;
+    uint32_t* dr = nullptr;
+    float* dd = nullptr;
+    uint32_t* dp = nullptr;
+    auto cleanup = [&]() {
+        if (dq) (void)hipFree(dq);
+        if (dr) (void)hipFree(dr);
+        if (dd) (void)hipFree(dd);
+        if (dp) (void)hipFree(dp);
+    };
+    const size_t qb = nq * ix->dim * sizeof(float), rb = nq * cfg->K * sizeof(uint32_t);
+    if (hipMalloc(&dq, qb) != hipSuccess || hipMalloc(&dr, rb) != hipSuccess ||
+        (dists && hipMalloc(&dd, rb) != hipSuccess) || hipMalloc(&dp, nq * 5 * 4) != hipSuccess) {
+        cleanup();
+        return fail(BS_ENOMEM, "hipMalloc of the query buffers failed");
+    }
+    hipError_t e = hipMemcpy(dq, queries, qb, hipMemcpyHostToDevice);
+    if (e != hipSuccess) {
+        cleanup();
+        return fail(BS_EHIP, std::string("query upload failed: ") + hipGetErrorString(e));
+    }
+    bs_stats st;
+    rc = bs_search_device(ix, cfg, dq, nq, dr, dd, dp, nullptr, 1, &st);
+    if (rc == BS_OK) {
+        e = hipMemcpy(results, dr, rb, hipMemcpyDeviceToHost);
+        if (e == hipSuccess && dists) e = hipMemcpy(dists, dd, rb, hipMemcpyDeviceToHost);
+        if (e != hipSuccess) rc = fail(BS_EHIP, std::string("result download failed: ") + hipGetErrorString(e));
+    }
+    cleanup();
+    if (rc == BS_OK && stats) *stats = st;
+    return rc;
+}

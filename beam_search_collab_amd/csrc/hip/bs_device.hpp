@@ -1,0 +1,602 @@
+// Device building blocks of the wave64 graph beam search (gfx950).
+//
+// One query runs on one 64-lane wavefront.  State per query:
+//   beam     T = 64*TR keys in VGPRs, sorted ascending, element e = r*64 + lane
+//            (register-major); key = (orderable(dist) << 32) | (id << 1) | expanded
+//   filter   visit filter in the wave's LDS slice (hash table or Bloom bits)
+//   query    the lane's float4 chunks of the query in VGPRs (L2 layout below)
+// Replaces the reference's TopKBuffer / VisitFilter / l2_warp / RabitQFastScan
+// (topk.cuh:16-49, visit_filter.cuh:10-30, l2.cuh:26-40, fastscan.cuh:19-369).
+#pragma once
+#include "wave.hpp"
+
+#include <float.h>
+#include <stdint.h>
+
+namespace bsd {
+
+using bsw::ballot;
+using bsw::lane_id;
+using bsw::readlane;
+using bsw::readlane64;
+using bsw::uniform;
+using bsw::wave_sync;
+
+constexpr uint64_t EMPTY_KEY = ~0ull;
+constexpr uint32_t INVALID = 0xFFFFFFFFu;
+
+// ---------------------------------------------------------------------------
+// keys: total order (dist, id, expanded).  The reference compares distances only
+// (topk_shared.cuh:463,499, ties unordered) and marks expansion in the id MSB
+// (topk_shared.cuh:370); here the CPU reference's (dist, node) order
+// (cpu_search_base.hpp:48-51) is the key order and the mark is the key's LSB.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ uint32_t orderable(float f) {
+    const uint32_t b = __float_as_uint(f);
+    return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+__device__ __forceinline__ float key_dist(uint64_t k) {
+    const uint32_t o = static_cast<uint32_t>(k >> 32);
+    return __uint_as_float((o & 0x80000000u) ? (o & 0x7FFFFFFFu) : ~o);
+}
+__device__ __forceinline__ uint64_t make_key(float d, uint32_t id) {
+    return (static_cast<uint64_t>(orderable(d)) << 32) | (static_cast<uint64_t>(id & 0x7FFFFFFFu) << 1);
+}
+__device__ __forceinline__ uint32_t key_id(uint64_t k) { return static_cast<uint32_t>(k >> 1) & 0x7FFFFFFFu; }
+
+// ---------------------------------------------------------------------------
+// beam merge: keep the T smallest of (beam U candidates).
+// Replaces SharedBitonicTopK::merge / RegBitonicTopK::merge (topk_shared.cuh:272-331).
+// Candidates live in registers ck[CR] (candidate index j = rc*64 + lane), `cmask[rc]`
+// says which lanes hold one.  Ranks are computed by broadcasting each candidate once:
+//   beam element e moves to e + #(candidates < beam[e]);
+//   candidate j moves to #(beam <= cand_j) + #(candidates before j in (key, index)).
+// These positions are a permutation of 0..T+c-1; the first T are scattered to LDS and
+// read back in register-major order.  The cost is ~(3*TR+6) instructions per candidate,
+// which suits the few new candidates a base-mode expansion produces.
+// ---------------------------------------------------------------------------
+template <int TR, int CR>
+__device__ __forceinline__ void beam_merge(uint64_t (&beam)[TR], const uint64_t (&ck)[CR],
+                                           const uint64_t (&cmask)[CR], uint32_t T,
+                                           uint64_t* lds_scratch) {
+    const uint32_t lane = lane_id();
+    uint32_t bpos[TR];
+#pragma unroll
+    for (int r = 0; r < TR; ++r) bpos[r] = static_cast<uint32_t>(r) * 64u + lane;
+    uint32_t cpos[CR];
+#pragma unroll
+    for (int rc = 0; rc < CR; ++rc) cpos[rc] = 0;
+
+#pragma unroll
+    for (int rj = 0; rj < CR; ++rj) {
+        uint64_t m = cmask[rj];
+        while (m) {
+            const uint32_t lj = static_cast<uint32_t>(__builtin_ctzll(m));
+            m &= m - 1;
+            const uint64_t kj = readlane64(ck[rj], lj);
+            const uint32_t jidx = static_cast<uint32_t>(rj) * 64u + lj;
+            uint32_t le = 0;
+#pragma unroll
+            for (int r = 0; r < TR; ++r) {
+                const bool lt = kj < beam[r];
+                bpos[r] += lt ? 1u : 0u;
+                le += static_cast<uint32_t>(__builtin_popcountll(~ballot(lt)));
+            }
+#pragma unroll
+            for (int rc = 0; rc < CR; ++rc) {
+                const uint32_t idx = static_cast<uint32_t>(rc) * 64u + lane;
+                const bool before = (kj < ck[rc]) || (kj == ck[rc] && jidx < idx);
+                cpos[rc] += before ? 1u : 0u;
+                if (rc == rj) cpos[rc] += (lane == lj) ? le : 0u;
+            }
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < TR; ++r)
+        if (bpos[r] < T) lds_scratch[bpos[r]] = beam[r];
+#pragma unroll
+    for (int rc = 0; rc < CR; ++rc)
+        if (((cmask[rc] >> lane) & 1ull) && cpos[rc] < T) lds_scratch[cpos[rc]] = ck[rc];
+    wave_sync();
+#pragma unroll
+    for (int r = 0; r < TR; ++r) {
+        const uint32_t e = static_cast<uint32_t>(r) * 64u + lane;
+        beam[r] = (e < T) ? lds_scratch[e] : EMPTY_KEY;
+    }
+    wave_sync();
+}
+
+// ---------------------------------------------------------------------------
+// pick<1> (topk_shared.cuh:335-380): mark the smallest unexpanded entry and return its
+// id (INVALID if none).  RUN = true (the rabitq beam may hold identical keys): of a run
+// of identical keys the last one is marked, which keeps the beam sorted.
+// ---------------------------------------------------------------------------
+template <int TR, bool RUN>
+__device__ __forceinline__ uint32_t beam_pick(uint64_t (&beam)[TR]) {
+    const uint32_t lane = lane_id();
+    int pr = -1;
+    uint32_t pl = 0;
+#pragma unroll
+    for (int r = 0; r < TR; ++r) {
+        const uint64_t m = ballot((static_cast<uint32_t>(beam[r]) & 1u) == 0u);
+        if (pr < 0 && m != 0) {
+            pr = r;
+            pl = static_cast<uint32_t>(__builtin_ctzll(m));
+        }
+    }
+    if (pr < 0) return INVALID;
+    uint64_t kp = 0;
+#pragma unroll
+    for (int r = 0; r < TR; ++r)
+        if (r == pr) kp = readlane64(beam[r], pl);
+    int qr = pr;
+    uint32_t ql = pl;
+    if constexpr (RUN) {
+#pragma unroll
+        for (int r = 0; r < TR; ++r) {
+            const uint64_t m = ballot(beam[r] == kp);
+            if (r >= pr && m != 0) {
+                qr = r;
+                ql = 63u - static_cast<uint32_t>(__builtin_clzll(m));
+            }
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < TR; ++r)
+        if (r == qr && lane == ql) beam[r] |= 1ull;
+    return key_id(kp);
+}
+
+// ---------------------------------------------------------------------------
+// bitonic sort of the 64*TR register-major keys, ascending (the rerank re-sort,
+// topk_shared.cuh:384-416).  Partners at distance >= 64 are other registers of the same
+// lane; closer partners are cross-lane exchanges (DPP / swizzle / bpermute).
+// ---------------------------------------------------------------------------
+template <int TR>
+__device__ __forceinline__ void bitonic_sort(uint64_t (&v)[TR]) {
+    const uint32_t lane = lane_id();
+    constexpr uint32_t N = 64u * TR;
+#pragma unroll
+    for (uint32_t k = 2; k <= N; k <<= 1) {
+#pragma unroll
+        for (uint32_t s = k >> 1; s >= 1; s >>= 1) {
+            if (s >= 64) {
+                const uint32_t rs = s / 64u;
+#pragma unroll
+                for (uint32_t r = 0; r < TR; ++r) {
+                    if ((r & rs) == 0) {
+                        const uint32_t r2 = r | rs;
+                        const uint32_t e = r * 64u + lane;
+                        const bool asc = (e & k) == 0;
+                        const uint64_t a = v[r], b = v[r2];
+                        const bool sw = asc ? (b < a) : (a < b);
+                        v[r] = sw ? b : a;
+                        v[r2] = sw ? a : b;
+                    }
+                }
+            } else {
+#pragma unroll
+                for (uint32_t r = 0; r < TR; ++r) {
+                    const uint64_t p = bsw::xor_lane64_rt(v[r], s);
+                    const uint32_t e = r * 64u + lane;
+                    const bool asc = (e & k) == 0;
+                    const bool lower = (lane & s) == 0;
+                    const bool keep_min = (lower == asc);
+                    const uint64_t mn = p < v[r] ? p : v[r];
+                    const uint64_t mx = p < v[r] ? v[r] : p;
+                    v[r] = keep_min ? mn : mx;
+                }
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// visit filters in the wave's LDS slice
+// ---------------------------------------------------------------------------
+
+// HashFilter (filter_hash.cuh:11-99): 2^bits slots, h = (k ^ (k >> bits)) & mask, linear
+// probing, empty = 0xFFFFFFFF.  `occ` counts occupied slots (wave-uniform).
+struct HashLds {
+    uint32_t* t;
+    uint32_t bits, size, mask;
+    uint32_t occ;
+
+    __device__ __forceinline__ uint32_t slot0(uint32_t k) const { return (k ^ (k >> bits)) & mask; }
+
+    __device__ __forceinline__ void clear() {
+        const uint32_t lane = lane_id();
+        for (uint32_t i = lane; i < size; i += 64) t[i] = INVALID;
+        occ = 0;
+        wave_sync();
+    }
+
+    // one key, sequential semantics, all lanes cooperate: probe 64 consecutive slots per
+    // step, first slot that holds k (present) or is empty (insert there).
+    // returns 1 if newly inserted; 0 if present or the table is full.
+    __device__ __forceinline__ uint32_t insert1(uint32_t k) {
+        const uint32_t lane = lane_id();
+        const uint32_t h = slot0(k);
+        for (uint32_t base = 0; base < size; base += 64) {
+            const uint32_t off = base + lane;
+            const uint32_t idx = (h + off) & mask;
+            const uint32_t s = (off < size) ? t[idx] : 0u;
+            const uint64_t hit = ballot(off < size && s == k);
+            const uint64_t emp = ballot(off < size && s == INVALID);
+            const uint64_t any = hit | emp;
+            if (any) {
+                const uint32_t first = static_cast<uint32_t>(__builtin_ctzll(any));
+                if ((hit >> first) & 1ull) return 0u;
+                if (lane == first) t[idx] = k;
+                wave_sync();
+                occ += 1;
+                return 1u;
+            }
+        }
+        return 0u;
+    }
+
+    __device__ __forceinline__ bool contains_lane(uint32_t k) const {
+        uint32_t idx = slot0(k);
+        for (uint32_t i = 0; i < size; ++i) {
+            const uint32_t s = t[idx];
+            if (s == k) return true;
+            if (s == INVALID) return false;
+            idx = (idx + 1) & mask;
+        }
+        return false;
+    }
+
+    // lane-parallel batch (one key per lane, INVALID = idle).  Sequential semantics in
+    // lane order: when the batch cannot fill the table, every lane inserts concurrently
+    // with LDS compare-and-swap (membership does not depend on the order); otherwise the
+    // keys are inserted one by one in lane order.  Returns 1 for newly inserted keys.
+    __device__ __forceinline__ uint32_t insert_batch(uint32_t k) {
+        const uint32_t lane = lane_id();
+        const bool valid = k != INVALID;
+        const uint64_t vm = ballot(valid);
+        const uint32_t nv = static_cast<uint32_t>(__builtin_popcountll(vm));
+        uint32_t isnew = 0;
+        if (nv == 0) return 0;
+        if (occ + nv <= size) {
+            uint32_t idx = slot0(k);
+            bool done = !valid;
+            for (uint32_t step = 0; step <= size; ++step) {
+                if (ballot(!done) == 0) break;
+                if (!done) {
+                    const uint32_t old = atomicCAS(&t[idx], INVALID, k);
+                    if (old == INVALID) {
+                        isnew = 1;
+                        done = true;
+                    } else if (old == k) {
+                        done = true;
+                    } else {
+                        idx = (idx + 1) & mask;
+                    }
+                }
+            }
+            wave_sync();
+            occ += static_cast<uint32_t>(__builtin_popcountll(ballot(isnew != 0)));
+        } else {
+            uint64_t m = vm;
+            while (m) {
+                const uint32_t l = static_cast<uint32_t>(__builtin_ctzll(m));
+                m &= m - 1;
+                const uint32_t r = insert1(readlane(k, l));
+                if (lane == l) isnew = r;
+            }
+        }
+        return isnew;
+    }
+};
+
+// BloomFilter (filter_bloom.cuh:13-131): 2^max(5, bits) bits, three hashes.  Batch
+// semantics (the reference's test-then-atomicOr races for a key inserted twice in one
+// step): a key is new iff its bits were not all set before the batch and it is the first
+// lane holding that value; then every key's bits are set.
+struct BloomLds {
+    uint32_t* w;
+    uint32_t bits, words, mask;
+
+    __device__ __forceinline__ void hashes(uint32_t key, uint32_t& h0, uint32_t& h1, uint32_t& h2) const {
+        uint32_t a = key;
+        a ^= a >> 16;
+        a *= 0x45d9f3bu;
+        a ^= a >> 16;
+        h0 = a & mask;
+        uint32_t b = key * 0x9e3779b9u;
+        b ^= b >> 16;
+        b *= 0x45d9f3bu;
+        b ^= b >> 16;
+        h1 = b & mask;
+        uint32_t c = key * 0x517cc1b7u;
+        c ^= c >> 16;
+        c *= 0x45d9f3bu;
+        c ^= c >> 16;
+        h2 = c & mask;
+    }
+
+    __device__ __forceinline__ void clear() {
+        const uint32_t lane = lane_id();
+        for (uint32_t i = lane; i < words; i += 64) w[i] = 0u;
+        wave_sync();
+    }
+
+    __device__ __forceinline__ bool test_lane(uint32_t k) const {
+        uint32_t h0, h1, h2;
+        hashes(k, h0, h1, h2);
+        return ((w[h0 >> 5] >> (h0 & 31)) & 1u) && ((w[h1 >> 5] >> (h1 & 31)) & 1u) &&
+               ((w[h2 >> 5] >> (h2 & 31)) & 1u);
+    }
+
+    __device__ __forceinline__ void set_lane(uint32_t k) {
+        uint32_t h0, h1, h2;
+        hashes(k, h0, h1, h2);
+        atomicOr(&w[h0 >> 5], 1u << (h0 & 31));
+        atomicOr(&w[h1 >> 5], 1u << (h1 & 31));
+        atomicOr(&w[h2 >> 5], 1u << (h2 & 31));
+    }
+
+    // keys k[rc] (rc-th register, index rc*64 + lane); returns new flags per register
+    template <int CR>
+    __device__ __forceinline__ void insert_batch(const uint32_t (&k)[CR], uint32_t (&isnew)[CR]) {
+        const uint32_t lane = lane_id();
+        bool present[CR], dup[CR];
+#pragma unroll
+        for (int rc = 0; rc < CR; ++rc) {
+            present[rc] = (k[rc] != INVALID) ? test_lane(k[rc]) : true;
+            dup[rc] = false;
+        }
+        // first occurrence: compare against every earlier valid key
+#pragma unroll
+        for (int rj = 0; rj < CR; ++rj) {
+            uint64_t m = ballot(k[rj] != INVALID);
+            while (m) {
+                const uint32_t lj = static_cast<uint32_t>(__builtin_ctzll(m));
+                m &= m - 1;
+                const uint32_t kj = readlane(k[rj], lj);
+                const uint32_t jidx = static_cast<uint32_t>(rj) * 64u + lj;
+#pragma unroll
+                for (int rc = 0; rc < CR; ++rc) {
+                    const uint32_t idx = static_cast<uint32_t>(rc) * 64u + lane;
+                    dup[rc] = dup[rc] || (k[rc] == kj && jidx < idx);
+                }
+            }
+        }
+        wave_sync();
+#pragma unroll
+        for (int rc = 0; rc < CR; ++rc) {
+            if (k[rc] != INVALID) set_lane(k[rc]);
+            isnew[rc] = (k[rc] != INVALID && !present[rc] && !dup[rc]) ? 1u : 0u;
+        }
+        wave_sync();
+    }
+};
+
+// ---------------------------------------------------------------------------
+// L2 (l2.cuh:26-40, rebuilt for wave64).  Rows are zero-padded to a multiple of 4
+// floats; a row is handled by G lanes (G = min(64, pow2ceil(dim/4))), lane `lig` of a
+// group accumulates chunks lig, lig+G, ... with one fma per component, and the group
+// sums its partials with an xor butterfly.  The same order is restated on the CPU
+// (orc_l2_wave in oracle/bs_oracle.c).
+// ---------------------------------------------------------------------------
+struct L2Shape {
+    uint32_t G, gshift, QR, chunks, rpp;  // rpp = rows per pass = 64 / G
+};
+
+template <int QMAX>
+__device__ __forceinline__ float l2_partial(const float4 (&q)[QMAX], const float* row, uint32_t lig,
+                                            const L2Shape& L, bool active) {
+    float p = 0.0f;
+    if (active) {
+        const float4* r4 = reinterpret_cast<const float4*>(row);
+#pragma unroll
+        for (int kk = 0; kk < QMAX; ++kk) {
+            const uint32_t j = lig + static_cast<uint32_t>(kk) * L.G;
+            if (static_cast<uint32_t>(kk) < L.QR && j < L.chunks) {
+                const float4 v = r4[j];
+                const float d0 = q[kk].x - v.x, d1 = q[kk].y - v.y, d2 = q[kk].z - v.z, d3 = q[kk].w - v.w;
+                p = __builtin_fmaf(d0, d0, p);
+                p = __builtin_fmaf(d1, d1, p);
+                p = __builtin_fmaf(d2, d2, p);
+                p = __builtin_fmaf(d3, d3, p);
+            }
+        }
+    }
+    return p;
+}
+
+// query chunks of this lane: chunk j = lig + k*G, components beyond dim are 0
+template <int QMAX>
+__device__ __forceinline__ void load_query(const float* qv, uint32_t dim, uint32_t lig, const L2Shape& L,
+                                           float4 (&q)[QMAX]) {
+#pragma unroll
+    for (int kk = 0; kk < QMAX; ++kk) {
+        const uint32_t j = lig + static_cast<uint32_t>(kk) * L.G;
+        float c[4];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            const uint32_t i = 4u * j + static_cast<uint32_t>(t);
+            c[t] = (static_cast<uint32_t>(kk) < L.QR && j < L.chunks && i < dim) ? qv[i] : 0.0f;
+        }
+        q[kk] = make_float4(c[0], c[1], c[2], c[3]);
+    }
+}
+
+// Distances of `cnt` rows whose ids are in lds_ids[0..cnt), written to lds_d[0..cnt).
+// Rows are `stride` floats apart.  Passes of rpp rows, PB passes in flight.
+template <int QMAX>
+__device__ __forceinline__ void l2_rows(const float4 (&q)[QMAX], const float* base, uint64_t stride,
+                                        const uint32_t* lds_ids, float* lds_d, uint32_t cnt,
+                                        const L2Shape& L) {
+    constexpr int PB = 4;
+    const uint32_t lane = lane_id();
+    const uint32_t g = lane >> L.gshift, lig = lane & (L.G - 1);
+    for (uint32_t j0 = 0; j0 < cnt; j0 += PB * L.rpp) {
+        float p[PB];
+#pragma unroll
+        for (int t = 0; t < PB; ++t) {
+            const uint32_t j = j0 + static_cast<uint32_t>(t) * L.rpp + g;
+            const bool act = j < cnt;
+            const uint32_t id = act ? lds_ids[j] : 0u;
+            p[t] = l2_partial<QMAX>(q, base + static_cast<uint64_t>(id) * stride, lig, L, act);
+        }
+#pragma unroll
+        for (int t = 0; t < PB; ++t) {
+            const float s = bsw::group_sum(p[t], L.G);
+            const uint32_t j = j0 + static_cast<uint32_t>(t) * L.rpp + g;
+            if (lig == 0 && j < cnt) lds_d[j] = s;
+        }
+    }
+    wave_sync();
+}
+
+// L2 of one row, result in every lane
+template <int QMAX>
+__device__ __forceinline__ float l2_one(const float4 (&q)[QMAX], const float* row, const L2Shape& L) {
+    const uint32_t lane = lane_id();
+    const uint32_t g = lane >> L.gshift, lig = lane & (L.G - 1);
+    float p = l2_partial<QMAX>(q, row, lig, L, g == 0);
+    p = bsw::group_sum(p, L.G);
+    return __uint_as_float(readlane(__float_as_uint(p), 0));
+}
+
+// ---------------------------------------------------------------------------
+// RaBitQ query quantization (fastscan.cuh:151-247) and bit planes (:292-329).
+// scratch: pdim floats of the wave's LDS; planes: 6*wpp words of LDS.
+// ---------------------------------------------------------------------------
+struct QuantOut {
+    float low, width;
+    int32_t sum_q;
+};
+
+__device__ __forceinline__ uint32_t dither_hash(uint32_t a, uint32_t b) {
+    a ^= b;
+    a ^= a >> 16;
+    a *= 0x45d9f3bu;
+    a ^= a >> 16;
+    a *= 0x45d9f3bu;
+    a ^= a >> 16;
+    return a;
+}
+
+__device__ __forceinline__ QuantOut quantize(const float* qv, const float* signs, uint32_t dim,
+                                             uint32_t pdim, uint32_t seed, float* scratch,
+                                             uint32_t* planes, uint8_t* codes_out) {
+    const uint32_t lane = lane_id();
+    for (uint32_t i = lane; i < pdim; i += 64) scratch[i] = (i < dim) ? __fmul_rn(qv[i], signs[i]) : 0.0f;
+    wave_sync();
+    uint32_t lshift = 0;
+    for (uint32_t len = 1; len < pdim; len <<= 1, ++lshift) {
+        for (uint32_t pi = lane; pi < (pdim >> 1); pi += 64) {
+            const uint32_t blk = pi >> lshift, j = pi & (len - 1);
+            const uint32_t i1 = (blk << (lshift + 1)) + j, i2 = i1 + len;
+            const float u = scratch[i1], v = scratch[i2];
+            scratch[i1] = __fadd_rn(u, v);
+            scratch[i2] = __fsub_rn(u, v);
+        }
+        wave_sync();
+    }
+    float mn = FLT_MAX, mx = -FLT_MAX;
+    for (uint32_t i = lane; i < pdim; i += 64) {
+        const float v = scratch[i];
+        mn = fminf(mn, v);
+        mx = fmaxf(mx, v);
+    }
+    mn = bsw::wave_min(mn);
+    mx = bsw::wave_max(mx);
+    const float low = __uint_as_float(uniform(__float_as_uint(mn)));
+    const float high = __uint_as_float(uniform(__float_as_uint(mx)));
+    const float width = __fdiv_rn(__fsub_rn(high, low), 63.0f);
+    const float inv_w = __fdiv_rn(1.0f, width);
+    uint32_t lsum = 0;
+    // codes are written back into scratch as words (one code per word) and into planes
+    for (uint32_t i0 = 0; i0 < pdim; i0 += 64) {
+        const uint32_t i = i0 + lane;
+        uint32_t c = 0;
+        if (i < pdim) {
+            const float x = __fmul_rn(__fsub_rn(scratch[i], low), inv_w);
+            const float u = static_cast<float>(dither_hash(seed, i) & 0xFFFFFFu) * (1.0f / 16777216.0f);
+            int qi = static_cast<int>(floorf(__fadd_rn(x, u)));
+            qi = qi < 0 ? 0 : (qi > 63 ? 63 : qi);
+            c = static_cast<uint32_t>(qi);
+            lsum += c;
+            if (codes_out) codes_out[i] = static_cast<uint8_t>(c);
+        }
+#pragma unroll
+        for (int b = 0; b < 6; ++b) {
+            const uint64_t m = ballot(((c >> b) & 1u) != 0u);
+            const uint32_t w0 = i0 >> 5;
+            if (lane == 0) planes[b * (pdim >> 5) + w0] = static_cast<uint32_t>(m);
+            if (lane == 0 && i0 + 32 < pdim) planes[b * (pdim >> 5) + w0 + 1] = static_cast<uint32_t>(m >> 32);
+        }
+    }
+    wave_sync();
+    const uint32_t s = bsw::group_sum_u32(lsum, 64);
+    QuantOut o;
+    o.low = low;
+    o.width = width;
+    o.sum_q = static_cast<int32_t>(uniform(s));
+    return o;
+}
+
+// est = tx + exact + fdq * width * ip + fvq * low, ip = 2 raw - sum_q; FLT_MAX when
+// tx == FLT_MAX or not finite (fastscan.cuh:361-366).  Evaluated in exactly that order
+// with no contraction.
+__device__ __forceinline__ float estimate(uint32_t raw, int32_t sum_q, float width, float low, float tx,
+                                          float fdq, float fvq, float exact) {
+    const float ip = static_cast<float>(static_cast<int32_t>(raw << 1) - sum_q);
+    const float a = __fadd_rn(tx, exact);
+    const float b = __fmul_rn(__fmul_rn(fdq, width), ip);
+    const float c = __fmul_rn(fvq, low);
+    float est = __fadd_rn(__fadd_rn(a, b), c);
+    if (tx == FLT_MAX || !__builtin_isfinite(est)) est = FLT_MAX;
+    return est;
+}
+
+// raw = sum_b 2^b * popcount(plane_b & code) over one code word (the lane's word)
+__device__ __forceinline__ uint32_t raw_word(const uint32_t (&pl)[6], uint32_t code) {
+    uint32_t r = 0;
+#pragma unroll
+    for (int b = 0; b < 6; ++b) r += static_cast<uint32_t>(__builtin_popcount(pl[b] & code)) << b;
+    return r;
+}
+
+// Integer fastscan sums of R neighbours (fastscan.cuh:346-355): raw[n] = sum over the
+// dims whose code bit is set of the query's 6-bit code.  Lane l works on neighbour
+// l / wpp, code word l % wpp (its plane words `pl` are those of word l % wpp); the wpp
+// word sums of a neighbour are combined by an xor butterfly (exact integer adds).
+// codes: R*wpp words (global), rawbuf: R words of LDS.
+__device__ __forceinline__ void raw_sums(const uint32_t (&pl)[6], const uint32_t* codes, uint32_t R,
+                                         uint32_t wpp, uint32_t* rawbuf) {
+    const uint32_t lane = lane_id();
+    const uint32_t npp = 64u / wpp;
+    const uint32_t npass = (R + npp - 1) / npp;
+    const uint32_t nl = lane / wpp, w = lane & (wpp - 1);
+    for (uint32_t t0 = 0; t0 < npass; t0 += 4) {
+        uint32_t acc[4];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            const uint32_t nb = (t0 + static_cast<uint32_t>(t)) * npp + nl;
+            const uint32_t code = (nb < R) ? codes[nb * wpp + w] : 0u;
+            acc[t] = raw_word(pl, code);
+        }
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            const uint32_t s = bsw::group_sum_u32(acc[t], wpp);
+            const uint32_t nb = (t0 + static_cast<uint32_t>(t)) * npp + nl;
+            if (w == 0 && nb < R) rawbuf[nb] = s;
+        }
+    }
+    wave_sync();
+}
+
+// the lane's six plane words (word index lane % wpp) after quantize()
+__device__ __forceinline__ void lane_planes(const uint32_t* planes, uint32_t wpp, uint32_t (&pl)[6]) {
+    const uint32_t w = lane_id() & (wpp - 1);
+#pragma unroll
+    for (int b = 0; b < 6; ++b) pl[b] = planes[b * wpp + w];
+    wave_sync();
+}
+
+}  // namespace bsd

@@ -1,0 +1,60 @@
+// Explicit search-kernel instances for one mode (BS_INST_MODE = 0 hash, 1 bloom,
+// 2 rabitq), compiled once per mode so the instances build in parallel.
+#include "bs_launch.hpp"
+
+#ifndef BS_INST_MODE
+#error "BS_INST_MODE must be defined"
+#endif
+
+namespace bsd {
+
+template <int TR, int CR, int QMAX>
+static hipError_t launch_one(const SearchParams& p, dim3 grid, dim3 block, size_t lds, hipStream_t s) {
+    auto k = search_kernel<TR, CR, QMAX, BS_INST_MODE>;
+    if (lds > 65536) {
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(k),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
+        if (e != hipSuccess) return e;
+    }
+    hipLaunchKernelGGL(k, grid, block, lds, s, p);
+    return hipGetLastError();
+}
+
+template <int TR, int CR>
+static hipError_t launch_q(const SearchParams& p, int QMAX, dim3 g, dim3 b, size_t lds, hipStream_t s) {
+    return QMAX == 1 ? launch_one<TR, CR, 1>(p, g, b, lds, s) : launch_one<TR, CR, 4>(p, g, b, lds, s);
+}
+
+template <int TR>
+static hipError_t launch_c(const SearchParams& p, int CR, int QMAX, dim3 g, dim3 b, size_t lds, hipStream_t s) {
+    return CR == 1 ? launch_q<TR, 1>(p, QMAX, g, b, lds, s) : launch_q<TR, 2>(p, QMAX, g, b, lds, s);
+}
+
+static hipError_t launch_any(const SearchParams& p, int TR, int CR, int QMAX, dim3 g, dim3 b, size_t lds,
+                             hipStream_t s) {
+    switch (TR) {
+    case 1: return launch_c<1>(p, CR, QMAX, g, b, lds, s);
+    case 2: return launch_c<2>(p, CR, QMAX, g, b, lds, s);
+    case 4: return launch_c<4>(p, CR, QMAX, g, b, lds, s);
+    default: return launch_c<8>(p, CR, QMAX, g, b, lds, s);
+    }
+}
+
+#if BS_INST_MODE == 0
+hipError_t launch_search_hash(const SearchParams& p, int TR, int CR, int QMAX, dim3 g, dim3 b, size_t lds,
+                              hipStream_t s) {
+    return launch_any(p, TR, CR, QMAX, g, b, lds, s);
+}
+#elif BS_INST_MODE == 1
+hipError_t launch_search_bloom(const SearchParams& p, int TR, int CR, int QMAX, dim3 g, dim3 b, size_t lds,
+                               hipStream_t s) {
+    return launch_any(p, TR, CR, QMAX, g, b, lds, s);
+}
+#else
+hipError_t launch_search_rabitq(const SearchParams& p, int TR, int CR, int QMAX, dim3 g, dim3 b, size_t lds,
+                                hipStream_t s) {
+    return launch_any(p, TR, CR, QMAX, g, b, lds, s);
+}
+#endif
+
+}  // namespace bsd

@@ -1,0 +1,329 @@
+// Search kernels: one query per 64-lane wavefront, NY wavefronts per workgroup.
+//
+// MODE_HASH / MODE_BLOOM restate gpu_search_base.cuh:120-247 and
+// gpu_search_warp.cuh:122-238 (the "base", "warpN" and "bwarpN" modes: the same loop,
+// only the visit filter differs); MODE_RABITQ restates gpu_search_rabitq.cuh:191-340.
+// The deterministic semantics (tie order, filter batch rules) are restated on the CPU
+// by oracle/bs_oracle.c.
+#pragma once
+#include "bs_device.hpp"
+
+namespace bsd {
+
+enum { MODE_HASH = 0, MODE_BLOOM = 1, MODE_RABITQ = 2 };
+
+struct SearchParams {
+    const float* vecs;      // n * dstride (zero-padded rows)
+    const uint32_t* edges;  // n * R
+    const uint32_t* recs;   // rabitq node records, n * rec_words
+    const float* signs;     // pdim
+    const float* queries;   // nq * dim
+    uint32_t* results;      // nq * K
+    float* dists;           // nq * K or null
+    uint32_t* per_query;    // nq * 5 or null: iterations, expansions, dist, est, rerank
+    uint64_t nq;
+    uint32_t dim, dstride, R, K, T;
+    uint32_t filter_bits;   // hash: log2 slots; bloom: log2 bits
+    uint32_t entry;
+    int32_t max_it, reset;
+    uint32_t pdim, wpp, rec_words, rec_ids, rec_fac, rec_codes;  // record offsets (words)
+    uint32_t lds_wave;      // bytes of LDS per wavefront
+    uint32_t off_filter, off_scratch, off_cand;  // byte offsets inside the wave slice
+    L2Shape L;
+};
+
+template <int TR, int CR, int QMAX, int MODE>
+__global__ void __launch_bounds__(512) search_kernel(const SearchParams p) {
+    extern __shared__ __attribute__((aligned(16))) char smem[];
+    const uint32_t lane = lane_id();
+    const uint32_t wave = threadIdx.x >> 6;
+    const uint64_t qid = static_cast<uint64_t>(blockIdx.x) * (blockDim.x >> 6) + wave;
+    if (qid >= p.nq) return;
+
+    char* my = smem + static_cast<size_t>(wave) * p.lds_wave;
+    uint64_t* scratch = reinterpret_cast<uint64_t*>(my + p.off_scratch);
+    uint32_t* cand_ids = reinterpret_cast<uint32_t*>(my + p.off_cand);
+    float* cand_d = reinterpret_cast<float*>(my + p.off_cand) + 64 * CR;
+
+    const L2Shape L = p.L;
+    const uint32_t lig = lane & (L.G - 1);
+    const float* qv = p.queries + qid * p.dim;
+    float4 q[QMAX];
+    load_query<QMAX>(qv, p.dim, lig, L, q);
+
+    const uint32_t T = p.T;
+    uint64_t beam[TR];
+#pragma unroll
+    for (int r = 0; r < TR; ++r) beam[r] = EMPTY_KEY;
+
+    uint32_t n_iter = 0, n_exp = 0, n_dist = 0, n_est = 0, n_rr = 0;
+
+    if constexpr (MODE != MODE_RABITQ) {
+        // ------------------------------------------------------------------ base
+        HashLds hf;
+        BloomLds bf;
+        if constexpr (MODE == MODE_HASH) {
+            hf.t = reinterpret_cast<uint32_t*>(my + p.off_filter);
+            hf.bits = p.filter_bits;
+            hf.size = 1u << p.filter_bits;
+            hf.mask = hf.size - 1;
+            hf.clear();
+        } else {
+            bf.w = reinterpret_cast<uint32_t*>(my + p.off_filter);
+            bf.bits = p.filter_bits;
+            bf.words = 1u << (p.filter_bits - 5);
+            bf.mask = (p.filter_bits >= 32) ? 0xFFFFFFFFu : ((1u << p.filter_bits) - 1);
+            bf.clear();
+        }
+        const float* vbase = p.vecs;
+        const uint64_t vstride = p.dstride;
+
+        // seed: the entry point is the only candidate (gpu_search_base.cuh:142-152)
+        uint64_t ck[CR];
+        uint64_t cm[CR];
+#pragma unroll
+        for (int rc = 0; rc < CR; ++rc) {
+            ck[rc] = EMPTY_KEY;
+            cm[rc] = 0;
+        }
+        {
+            const float d0 = l2_one<QMAX>(q, vbase + static_cast<uint64_t>(p.entry) * vstride, L);
+            ck[0] = (lane == 0) ? make_key(d0, p.entry) : EMPTY_KEY;
+            cm[0] = 1ull;
+            n_dist = 1;
+            if constexpr (MODE == MODE_HASH) {
+                hf.insert1(p.entry);
+            } else {
+                if (lane == 0) bf.set_lane(p.entry);
+                wave_sync();
+            }
+        }
+        int32_t until_reset = p.reset;
+
+        for (int32_t iter = 0; iter < p.max_it; ++iter) {
+            ++n_iter;
+            // merge candidates into the beam
+            bool any = false;
+#pragma unroll
+            for (int rc = 0; rc < CR; ++rc) any = any || (cm[rc] != 0);
+            if (any) beam_merge<TR, CR>(beam, ck, cm, T, scratch);
+#pragma unroll
+            for (int rc = 0; rc < CR; ++rc) cm[rc] = 0;
+
+            // forgettable filter: clear and re-insert the beam ids (gpu_search_base.cuh:173-181)
+            if (p.reset > 0 && --until_reset == 0) {
+                until_reset = p.reset;
+                if constexpr (MODE == MODE_HASH) {
+                    hf.clear();
+#pragma unroll
+                    for (int r = 0; r < TR; ++r) {
+                        const uint32_t id = (beam[r] == EMPTY_KEY) ? INVALID : key_id(beam[r]);
+                        hf.insert_batch(id);
+                    }
+                } else {
+                    bf.clear();
+#pragma unroll
+                    for (int r = 0; r < TR; ++r)
+                        if (beam[r] != EMPTY_KEY) bf.set_lane(key_id(beam[r]));
+                    wave_sync();
+                }
+            }
+
+            // pick the best unexpanded node
+            const uint32_t parent = beam_pick<TR, false>(beam);
+            if (parent == INVALID) break;
+            ++n_exp;
+
+            // expand: neighbours through the filter
+            const uint32_t* row = p.edges + static_cast<uint64_t>(parent) * p.R;
+            uint32_t child[CR], isnew[CR];
+#pragma unroll
+            for (int rc = 0; rc < CR; ++rc) {
+                const uint32_t i = static_cast<uint32_t>(rc) * 64u + lane;
+                child[rc] = (i < p.R) ? row[i] : INVALID;
+            }
+            if constexpr (MODE == MODE_HASH) {
+#pragma unroll
+                for (int rc = 0; rc < CR; ++rc) isnew[rc] = hf.insert_batch(child[rc]);
+            } else {
+                bf.insert_batch<CR>(child, isnew);
+            }
+            // compact the new neighbours into the LDS id list
+            uint32_t c = 0;
+#pragma unroll
+            for (int rc = 0; rc < CR; ++rc) {
+                const uint64_t m = ballot(isnew[rc] != 0);
+                if (isnew[rc]) cand_ids[c + bsw::lanes_below(m)] = child[rc];
+                c += static_cast<uint32_t>(__builtin_popcountll(m));
+            }
+            wave_sync();
+            if (c == 0) continue;
+            n_dist += c;
+            l2_rows<QMAX>(q, vbase, vstride, cand_ids, cand_d, c, L);
+#pragma unroll
+            for (int rc = 0; rc < CR; ++rc) {
+                const uint32_t j = static_cast<uint32_t>(rc) * 64u + lane;
+                const bool v = j < c;
+                ck[rc] = v ? make_key(cand_d[j], cand_ids[j]) : EMPTY_KEY;
+                cm[rc] = ballot(v);
+            }
+            wave_sync();
+        }
+        {
+            bool any = false;
+#pragma unroll
+            for (int rc = 0; rc < CR; ++rc) any = any || (cm[rc] != 0);
+            if (any) beam_merge<TR, CR>(beam, ck, cm, T, scratch);
+        }
+        // flush the K smallest, ascending
+        uint32_t* out = p.results + qid * p.K;
+        float* dout = p.dists ? p.dists + qid * p.K : nullptr;
+#pragma unroll
+        for (int r = 0; r < TR; ++r) {
+            const uint32_t e = static_cast<uint32_t>(r) * 64u + lane;
+            if (e < p.K) {
+                out[e] = (beam[r] == EMPTY_KEY) ? INVALID : key_id(beam[r]);
+                if (dout) dout[e] = (beam[r] == EMPTY_KEY) ? FLT_MAX : key_dist(beam[r]);
+            }
+        }
+    } else {
+        // ---------------------------------------------------------------- rabitq
+        HashLds hf;
+        hf.t = reinterpret_cast<uint32_t*>(my + p.off_filter);
+        hf.bits = p.filter_bits;
+        hf.size = 1u << p.filter_bits;
+        hf.mask = hf.size - 1;
+        const uint32_t wpp = p.wpp;
+        const uint64_t rstride = p.rec_words;
+        const float* rbase = reinterpret_cast<const float*>(p.recs);
+
+        // quantize the query; the lane's plane words for word index (lane % wpp)
+        uint32_t pl[6];
+        QuantOut qo;
+        {
+            float* qscr = reinterpret_cast<float*>(scratch);
+            uint32_t* planes = reinterpret_cast<uint32_t*>(my + p.off_scratch + 4u * p.pdim);
+            qo = quantize(qv, p.signs, p.dim, p.pdim, 0u, qscr, planes, nullptr);
+            lane_planes(planes, wpp, pl);
+        }
+        hf.clear();
+
+        // entry point with its exact distance (gpu_search_rabitq.cuh:210-223)
+        {
+            const float d0 = l2_one<QMAX>(q, rbase + static_cast<uint64_t>(p.entry) * rstride, L);
+            n_dist = 1;
+            uint64_t ck[1] = {lane == 0 ? make_key(d0, p.entry) : EMPTY_KEY};
+            uint64_t cm[1] = {1ull};
+            beam_merge<TR, 1>(beam, ck, cm, T, scratch);
+        }
+        uint32_t* rawbuf = cand_ids;
+
+        for (int32_t iter = 0; iter < p.max_it; ++iter) {
+            ++n_iter;
+            const uint32_t parent = beam_pick<TR, true>(beam);
+            if (parent == INVALID) break;
+            if (!hf.insert1(parent)) continue;  // already expanded (gpu_search_rabitq.cuh:249-252)
+            ++n_exp;
+            const uint32_t* rec = p.recs + static_cast<uint64_t>(parent) * rstride;
+            // neighbour ids, filtered by the expanded set
+            uint32_t child[CR];
+            bool valid[CR];
+#pragma unroll
+            for (int rc = 0; rc < CR; ++rc) {
+                const uint32_t i = static_cast<uint32_t>(rc) * 64u + lane;
+                child[rc] = (i < p.R) ? rec[p.rec_ids + i] : INVALID;
+            }
+            const float exact = l2_one<QMAX>(q, reinterpret_cast<const float*>(rec), L);
+            ++n_dist;
+#pragma unroll
+            for (int rc = 0; rc < CR; ++rc) valid[rc] = child[rc] != INVALID && !hf.contains_lane(child[rc]);
+            raw_sums(pl, rec + p.rec_codes, p.R, wpp, rawbuf);
+            uint64_t ck[CR], cm[CR];
+            uint32_t nv = 0;
+#pragma unroll
+            for (int rc = 0; rc < CR; ++rc) {
+                const uint32_t i = static_cast<uint32_t>(rc) * 64u + lane;
+                uint64_t k = EMPTY_KEY;
+                if (valid[rc]) {
+                    const float* fac = reinterpret_cast<const float*>(rec + p.rec_fac);
+                    const float est = estimate(rawbuf[i], qo.sum_q, qo.width, qo.low, fac[i], fac[p.R + i],
+                                               fac[2 * p.R + i], exact);
+                    k = make_key(est, child[rc]);
+                }
+                ck[rc] = k;
+                cm[rc] = ballot(valid[rc]);
+                nv += static_cast<uint32_t>(__builtin_popcountll(cm[rc]));
+            }
+            wave_sync();
+            n_est += nv;
+            beam_merge<TR, CR>(beam, ck, cm, T, scratch);
+        }
+
+        // exact rerank of every beam slot (gpu_search_rabitq.cuh:314-317)
+        uint32_t* ids = reinterpret_cast<uint32_t*>(scratch);
+        float* rd = reinterpret_cast<float*>(scratch) + 64 * TR;
+        uint32_t nvb = 0;
+#pragma unroll
+        for (int r = 0; r < TR; ++r) {
+            const uint32_t e = static_cast<uint32_t>(r) * 64u + lane;
+            ids[e] = (beam[r] == EMPTY_KEY) ? INVALID : key_id(beam[r]);
+            nvb += static_cast<uint32_t>(__builtin_popcountll(ballot(beam[r] != EMPTY_KEY)));
+        }
+        wave_sync();
+        // the valid entries are the first nvb (the beam is sorted, empty keys last)
+        l2_rows<QMAX>(q, rbase, rstride, ids, rd, nvb, L);
+        n_rr += nvb;
+#pragma unroll
+        for (int r = 0; r < TR; ++r) {
+            const uint32_t e = static_cast<uint32_t>(r) * 64u + lane;
+            beam[r] = (e < nvb) ? make_key(rd[e], ids[e]) : EMPTY_KEY;
+        }
+        wave_sync();
+        bitonic_sort<TR>(beam);
+
+        // dedup flush from the smallest (gpu_search_rabitq.cuh:319-339): identical ids
+        // carry identical exact distances and are adjacent; the flush's hash set accepts
+        // at most `size` distinct ids.
+        uint32_t* out = p.results + qid * p.K;
+        float* dout = p.dists ? p.dists + qid * p.K : nullptr;
+        const uint32_t limit = (p.K < hf.size) ? p.K : hf.size;
+        uint32_t written = 0;
+        uint32_t prev_last = INVALID;  // id of element 64*r - 1
+        uint32_t wpos[TR];
+        bool keep[TR];
+#pragma unroll
+        for (int r = 0; r < TR; ++r) {
+            const uint32_t id = (beam[r] == EMPTY_KEY) ? INVALID : key_id(beam[r]);
+            uint32_t prv = bsw::prev_lane(id);
+            if (lane == 0) prv = prev_last;
+            keep[r] = (id != INVALID) && (id != prv);
+            const uint64_t km = ballot(keep[r]);
+            wpos[r] = written + bsw::lanes_below(km);
+            written += static_cast<uint32_t>(__builtin_popcountll(km));
+            prev_last = readlane(id, 63);
+        }
+        const uint32_t nw = written < limit ? written : limit;
+        for (uint32_t e = nw + lane; e < p.K; e += 64) {
+            out[e] = INVALID;
+            if (dout) dout[e] = FLT_MAX;
+        }
+#pragma unroll
+        for (int r = 0; r < TR; ++r) {
+            if (keep[r] && wpos[r] < nw) {
+                out[wpos[r]] = key_id(beam[r]);
+                if (dout) dout[wpos[r]] = key_dist(beam[r]);
+            }
+        }
+    }
+
+    if (p.per_query && lane == 0) {
+        uint32_t* pq = p.per_query + qid * 5;
+        pq[0] = n_iter;
+        pq[1] = n_exp;
+        pq[2] = n_dist;
+        pq[3] = n_est;
+        pq[4] = n_rr;
+    }
+}
+
+}  // namespace bsd

@@ -1,0 +1,150 @@
+// Wave64 building blocks for gfx950 (CDNA4): lane exchanges, ballots, wave-scope sync.
+//
+// Exchanges used by the reductions and the bitonic sorter:
+//   xor 1, 2      DPP quad_perm                      (VALU, no LDS traffic)
+//   xor 4, 8      two DPP mirrors (row_half_mirror/row_mirror composed with quad reverse)
+//   xor 16        ds_swizzle bit-mask mode (within 32-lane halves)
+//   xor 32        ds_bpermute
+//   shift by one  ds_bpermute
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace bsw {
+
+__device__ __forceinline__ uint32_t lane_id() {
+    return __builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u));
+}
+
+__device__ __forceinline__ uint64_t ballot(bool p) { return __builtin_amdgcn_ballot_w64(p); }
+
+// number of set bits of m below this lane
+__device__ __forceinline__ uint32_t lanes_below(uint64_t m) {
+    return __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(m >> 32),
+                                     __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(m), 0u));
+}
+
+__device__ __forceinline__ uint32_t readlane(uint32_t v, uint32_t l) {
+    return static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v), static_cast<int>(l)));
+}
+__device__ __forceinline__ uint64_t readlane64(uint64_t v, uint32_t l) {
+    const uint32_t lo = readlane(static_cast<uint32_t>(v), l);
+    const uint32_t hi = readlane(static_cast<uint32_t>(v >> 32), l);
+    return (static_cast<uint64_t>(hi) << 32) | lo;
+}
+__device__ __forceinline__ uint32_t uniform(uint32_t v) {
+    return static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(v)));
+}
+
+// Orders LDS traffic of the wave: every lane's earlier LDS writes are visible to every
+// lane's later LDS reads, and the compiler may not move LDS accesses across it.
+__device__ __forceinline__ void wave_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// DPP controls (GFX9 encoding)
+constexpr int DPP_QP_XOR1 = 0xB1;   // quad_perm [1,0,3,2]
+constexpr int DPP_QP_XOR2 = 0x4E;   // quad_perm [2,3,0,1]
+constexpr int DPP_QP_XOR3 = 0x1B;   // quad_perm [3,2,1,0]
+constexpr int DPP_HALF_MIRROR = 0x141;  // lane i -> 7-i within 8
+constexpr int DPP_MIRROR = 0x140;       // lane i -> 15-i within 16
+
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp(uint32_t v) {
+    return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), CTRL, 0xF, 0xF, false));
+}
+
+// value of lane (this lane ^ S)
+template <int S>
+__device__ __forceinline__ uint32_t xor_lane(uint32_t v) {
+    if constexpr (S == 1) {
+        return dpp<DPP_QP_XOR1>(v);
+    } else if constexpr (S == 2) {
+        return dpp<DPP_QP_XOR2>(v);
+    } else if constexpr (S == 4) {
+        return dpp<DPP_QP_XOR3>(dpp<DPP_HALF_MIRROR>(v));  // (i ^ 7) ^ 3 = i ^ 4
+    } else if constexpr (S == 8) {
+        return dpp<DPP_HALF_MIRROR>(dpp<DPP_MIRROR>(v));   // (i ^ 15) ^ 7 = i ^ 8
+    } else if constexpr (S == 16) {
+        return static_cast<uint32_t>(__builtin_amdgcn_ds_swizzle(static_cast<int>(v), 0x401F));
+    } else {
+        static_assert(S == 32, "xor distance must be a power of two below 64");
+        return static_cast<uint32_t>(
+            __builtin_amdgcn_ds_bpermute(static_cast<int>((lane_id() ^ 32u) << 2), static_cast<int>(v)));
+    }
+}
+
+template <int S>
+__device__ __forceinline__ float xor_lane_f(float v) {
+    return __uint_as_float(xor_lane<S>(__float_as_uint(v)));
+}
+template <int S>
+__device__ __forceinline__ uint64_t xor_lane64(uint64_t v) {
+    const uint32_t lo = xor_lane<S>(static_cast<uint32_t>(v));
+    const uint32_t hi = xor_lane<S>(static_cast<uint32_t>(v >> 32));
+    return (static_cast<uint64_t>(hi) << 32) | lo;
+}
+
+// run-time distance (folded when the call is unrolled with a constant s)
+__device__ __forceinline__ uint64_t xor_lane64_rt(uint64_t v, uint32_t s) {
+    switch (s) {
+    case 1: return xor_lane64<1>(v);
+    case 2: return xor_lane64<2>(v);
+    case 4: return xor_lane64<4>(v);
+    case 8: return xor_lane64<8>(v);
+    case 16: return xor_lane64<16>(v);
+    default: return xor_lane64<32>(v);
+    }
+}
+
+// value of lane (this lane - 1); lane 0 gets lane 63's value
+__device__ __forceinline__ uint32_t prev_lane(uint32_t v) {
+    return static_cast<uint32_t>(
+        __builtin_amdgcn_ds_bpermute(static_cast<int>(((lane_id() + 63u) & 63u) << 2), static_cast<int>(v)));
+}
+
+// Sum over aligned groups of G lanes (G a power of two <= 64) by an xor butterfly:
+// p_l += p_{l^s} for s = 1, 2, ..., G/2.  Every lane of a group ends with the same
+// value (float addition is commutative).  All 64 lanes must be active.
+__device__ __forceinline__ float group_sum(float p, uint32_t G) {
+    if (G > 1) p = p + xor_lane_f<1>(p);
+    if (G > 2) p = p + xor_lane_f<2>(p);
+    if (G > 4) p = p + xor_lane_f<4>(p);
+    if (G > 8) p = p + xor_lane_f<8>(p);
+    if (G > 16) p = p + xor_lane_f<16>(p);
+    if (G > 32) p = p + xor_lane_f<32>(p);
+    return p;
+}
+
+__device__ __forceinline__ uint32_t group_sum_u32(uint32_t p, uint32_t G) {
+    if (G > 1) p += xor_lane<1>(p);
+    if (G > 2) p += xor_lane<2>(p);
+    if (G > 4) p += xor_lane<4>(p);
+    if (G > 8) p += xor_lane<8>(p);
+    if (G > 16) p += xor_lane<16>(p);
+    if (G > 32) p += xor_lane<32>(p);
+    return p;
+}
+
+__device__ __forceinline__ float wave_min(float v) {
+    v = fminf(v, xor_lane_f<1>(v));
+    v = fminf(v, xor_lane_f<2>(v));
+    v = fminf(v, xor_lane_f<4>(v));
+    v = fminf(v, xor_lane_f<8>(v));
+    v = fminf(v, xor_lane_f<16>(v));
+    v = fminf(v, xor_lane_f<32>(v));
+    return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+    v = fmaxf(v, xor_lane_f<1>(v));
+    v = fmaxf(v, xor_lane_f<2>(v));
+    v = fmaxf(v, xor_lane_f<4>(v));
+    v = fmaxf(v, xor_lane_f<8>(v));
+    v = fmaxf(v, xor_lane_f<16>(v));
+    v = fmaxf(v, xor_lane_f<32>(v));
+    return v;
+}
+
+}  // namespace bsw

@@ -1,0 +1,9 @@
+// Shared helpers of the host library (error text, thread count).
+#pragma once
+#include <string>
+
+namespace bsh {
+extern thread_local std::string g_err;
+int fail(int code, const std::string& msg);
+int n_threads(int threads);
+}  // namespace bsh

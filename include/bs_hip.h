@@ -1,0 +1,156 @@
+/*
+ * bs_hip.h -- C-ABI of the MI355X (gfx950) graph beam search: libbs_hip.so.
+ *
+ * This is the drop-in boundary for the reference's GPU search path.  The reference has
+ * no FFI of its own: its boundary is C++ templates inside src/gpu_cli.cu
+ *   host  run_base / run_warp<NY,Filter> / run_rabitq<NY>   (src/gpu_cli.cu:140-349)
+ *   ->    kernel_{base,warp,rabitq}_search<<<...>>>          (src/gpu_cli.cu:87-136)
+ *   ->    Searcher::search(query, results, K)                (gpu_search_base.cuh:65,
+ *                                                             gpu_search_warp.cuh:54,
+ *                                                             gpu_search_rabitq.cuh:65)
+ * with the device-resident index of GPUGraph / GPURabitq (gpu_graph.cuh:81-146,
+ * rabitq.cuh:67-110).  The entry points below replace exactly that layer; a C++ host
+ * (gpu_cli), Python (ctypes) or any other FFI binds them.  No HIP or torch types
+ * appear in the signatures: streams are passed as void* (a hipStream_t, or NULL for the
+ * null stream).
+ *
+ * Conventions
+ *   - return 0 on success, a negative BS_E* code on error; bs_last_error() returns the
+ *     text of the calling thread's last error.  No C++ exception crosses the ABI.
+ *   - calls on one bs_index must be externally serialised; separate indexes are
+ *     independent.
+ *   - results are node ids in ascending (distance, id) order, 0xFFFFFFFF where fewer
+ *     than K nodes were found (the reference writes the K results in descending order,
+ *     topk_shared.cuh:420-429; the CPU reference cpu_cli writes them ascending).
+ */
+#ifndef BS_HIP_H
+#define BS_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define BS_OK 0
+#define BS_EINVAL (-1)  /* bad argument / unsupported configuration          */
+#define BS_EHIP (-2)    /* a HIP runtime call failed                          */
+#define BS_ENOMEM (-3)  /* device or host allocation failed                   */
+#define BS_ENODEV (-4)  /* no usable gfx950 device                            */
+
+typedef struct bs_index_s* bs_index;
+
+/* Search modes (src/gpu_cli.cu:427-477 "mode"):
+ *   BS_BASE        "base"    one query per workgroup, hash filter
+ *   BS_GROUP       "warpN"   N = queries_per_group queries per workgroup, hash filter
+ *   BS_GROUP_BLOOM "bwarpN"  as BS_GROUP with the Bloom visit filter
+ *   BS_RABITQ      "rabitq"  RaBitQ estimates + exact rerank (needs bs_index_attach_rabitq)
+ * Every mode runs one query per 64-lane wavefront.  base/warpN give identical results
+ * (same semantics); they differ only in how many wavefronts share a workgroup. */
+typedef enum { BS_BASE = 0, BS_GROUP = 1, BS_GROUP_BLOOM = 2, BS_RABITQ = 3 } bs_mode;
+
+/* GPUBaseSearchCfg (gpu_search_base.cuh:17-23) / GPURabitqSearchCfg
+ * (gpu_search_rabitq.cuh:21-26) plus the mode and K of gpu_cli's JSON "search" object
+ * (src/gpu_cli.cu:414-452). */
+typedef struct {
+    int32_t mode;               /* bs_mode                                             */
+    uint32_t queries_per_group; /* wavefronts (queries) per workgroup: 1,2,4,8; 0 -> 1  */
+    uint32_t K;                 /* results per query (>= 1, <= topk_size)              */
+    uint32_t topk_size;         /* beam slots, 1..512                                  */
+    uint32_t filter_capacity;   /* hash slots / Bloom bits (rounded up to a power of 2)*/
+    uint32_t entry_point;       /* start node (< n)                                    */
+    int32_t max_iterations;     /* >= 0                                                */
+    int32_t reset_interval;     /* forgettable-filter reset period; 0 = never (>= 0)   */
+} bs_search_cfg;
+
+/* Work counters summed over the queries of one call (the byte model of the roofline:
+ * base  B_q = 4d + E*4R + D*4d + 4K;
+ * rabitq B_q = 4d + 4pdim + E*(4R + 4R*wpp + 12R + 4d) + T_r*4d + 4K). */
+typedef struct {
+    double kernel_ms;       /* search kernel time (HIP events on the launch stream)     */
+    uint64_t iterations;    /* beam-loop iterations                                    */
+    uint64_t expansions;    /* E: adjacency rows (rabitq: node records) read           */
+    uint64_t dist_evals;    /* D: exact L2 evaluations during the search               */
+    uint64_t est_evals;     /* RaBitQ estimates                                        */
+    uint64_t rerank_evals;  /* T_r: exact L2 evaluations of the final rerank           */
+} bs_stats;
+
+/* Upload a graph: vecs n*dim f32, edges n*degree u32 (ids < n or 0xFFFFFFFF).
+ * Replaces GPUGraph(const CPUGraph&) (gpu_graph.cuh:81-146).  Validates every edge on
+ * the host.  dim 1..1024, degree 1..128, n < 2^31. */
+int bs_index_create(const float* vecs, const uint32_t* edges, uint64_t n, uint32_t dim,
+                    uint32_t degree, bs_index* out);
+
+/* Attach RaBitQ data: codes n*degree*(padded_dim/32) u32, factors n*3*degree f32
+ * (tx | fdq | fvq per node), signs padded_dim f32.  Replaces GPURabitq(const
+ * CPURabitqData&) (rabitq.cuh:67-110).  padded_dim must be pow2ceil(dim) and >= 32. */
+int bs_index_attach_rabitq(bs_index idx, const uint32_t* codes, const float* factors,
+                           const float* signs, uint32_t padded_dim);
+
+/* Search nq host-resident queries (nq*dim f32); results (host, nq*K u32) and optional
+ * dists (host, nq*K f32, NULL allowed) are written.  Replaces one timed launch of
+ * run_base / run_warp / run_rabitq (src/gpu_cli.cu:140-349) including the query upload
+ * and result download of gpu_cli main (src/gpu_cli.cu:399-421,481). stats nullable. */
+int bs_search(bs_index idx, const bs_search_cfg* cfg, const float* queries, uint64_t nq,
+              uint32_t* results, float* dists, bs_stats* stats);
+
+/* Same search with device-resident buffers (queries nq*dim f32, results nq*K u32,
+ * dists nq*K f32 or NULL, per_query nq*5 u32 counters {iterations, expansions,
+ * dist_evals, est_evals, rerank_evals} or NULL), launched on `stream` (hipStream_t or
+ * NULL).  Allocates no device memory.  Asynchronous unless sync != 0; with sync != 0
+ * stats (nullable) gets kernel_ms and, when per_query is given, the summed counters. */
+int bs_search_device(bs_index idx, const bs_search_cfg* cfg, const float* d_queries,
+                     uint64_t nq, uint32_t* d_results, float* d_dists, uint32_t* d_per_query,
+                     void* stream, int sync, bs_stats* stats);
+
+/* Device pointers of the uploaded index (for tests and profilers). */
+int bs_index_info(bs_index idx, uint64_t* n, uint32_t* dim, uint32_t* degree,
+                  uint32_t* padded_dim, int* has_rabitq);
+
+void bs_index_destroy(bs_index idx);
+const char* bs_last_error(void);
+
+/* ---- primitive entry points (parity tests of the device building blocks) ----------
+ * Each runs the same device functions the search kernels use, on one wavefront per
+ * instance.  All buffers are host memory. */
+
+/* L2 of pairs (query qi[p], node ni[p]) with the search kernels' wave64 order.
+ * Replaces l2_warp (l2.cuh:26-40). */
+int bs_debug_l2(bs_index idx, const float* queries, uint64_t nq, const uint32_t* qi,
+                const uint32_t* ni, uint64_t npairs, float* out);
+
+/* Quantize one query (sign flip, WHT, dithered 6-bit codes, seed) and estimate nn
+ * neighbours: codes_nbr nn*(pdim/32) u32, factors 3*degree f32 (tx|fdq|fvq, nn <= 64,
+ * nn <= degree).  Outputs: codes_out pdim u8, scal_out {low, width} f32, sum_q_out,
+ * raw_out nn u32, est_out nn f32.  Replaces RabitqQuantizer::quantize + RabitQFastScan
+ * (fastscan.cuh:151-369). */
+int bs_debug_fastscan(const float* query, const float* signs, uint32_t dim, uint32_t seed,
+                      const uint32_t* codes_nbr, const float* factors, uint32_t nn,
+                      uint32_t degree, float exact, uint8_t* codes_out, float* scal_out,
+                      int32_t* sum_q_out, uint32_t* raw_out, float* est_out);
+
+/* Beam harness: topk slots; nbatch batches of bsize (<= 256) candidate keys
+ * ((orderable(dist) << 32) | (id << 1), 0xFFFF...FF = no candidate) merged in order;
+ * after each batch `picks` picks (pick_run = 1: the rabitq rule for identical keys).
+ * picked nbatch*picks ids (0xFFFFFFFF = nothing to pick), beam_out topk keys.
+ * Replaces SharedBitonicTopK / RegBitonicTopK merge + pick (topk_shared.cuh:272-380,
+ * topk_reg.cuh). */
+int bs_debug_beam(uint32_t topk, const uint64_t* keys, uint32_t nbatch, uint32_t bsize,
+                  uint32_t picks, int pick_run, uint32_t* picked, uint64_t* beam_out);
+
+/* Full sort of n (<= 512) keys ascending (the rerank sorter; replaces the bitonic
+ * re-sort of topk_shared.cuh:384-416). */
+int bs_debug_sort(const uint64_t* keys, uint32_t n, uint64_t* out);
+
+/* Visit filters: nbatch lane-parallel batches of bsize (<= 64) inserts (0xFFFFFFFF =
+ * idle lane), then nquery contains().  bloom = 0: HashFilter (filter_hash.cuh),
+ * 1: BloomFilter (filter_bloom.cuh). */
+int bs_debug_filter(int bloom, uint32_t capacity, const uint32_t* keys, uint32_t nbatch,
+                    uint32_t bsize, uint32_t* out_new, const uint32_t* qkeys, uint32_t nquery,
+                    uint32_t* out_contains);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,129 @@
+"""Device building blocks on the MI355X against the CPU oracle (bit-exact) and closed
+forms.  Mirrors the reference unit tests: test_fastscan.cu, test_filter_hash.cu,
+test_topk_*_merge.cu, *_no_dup.cu, test_topk_reg_pick_order.cu, *_bitonic_sort*.cu."""
+import numpy as np
+import pytest
+
+from conftest import load_fastscan_golden
+from beam_search_collab_amd import host, search
+from oracle import pyoracle as po
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("seed", [42, 123])
+def test_fastscan_matches_reference_golden(gpu, seed):
+    for r in load_fastscan_golden(seed):
+        codes, low, width, sq, raw, est = search.debug_fastscan(
+            r["query"], r["signs"], r["dim"], r["seed"], r["nbrs"], r["factors"], r["nn"], r["degree"], r["exact"])
+        assert np.array_equal(codes, r["codes"]), r["dim"]
+        assert np.float32(low).tobytes() == r["low"].tobytes()
+        assert np.float32(width).tobytes() == r["width"].tobytes()
+        assert sq == r["sum_q"]
+        assert np.array_equal(raw, r["raw"])
+        assert est.tobytes() == r["est"].tobytes(), (r["dim"], est, r["est"])
+
+
+@pytest.mark.parametrize("dim", [1, 3, 16, 25, 32, 100, 128, 200, 384, 960, 1024])
+def test_l2_wave_order(gpu, dim):
+    rng = np.random.default_rng(dim)
+    n, nq = 300, 7
+    base = rng.standard_normal((n, dim)).astype(np.float32) * 10
+    q = rng.standard_normal((nq, dim)).astype(np.float32) * 10
+    g = search.GPUGraph(base, np.zeros((n, 4), np.uint32))
+    qi = rng.integers(0, nq, 500).astype(np.uint32)
+    ni = rng.integers(0, n, 500).astype(np.uint32)
+    got = search.debug_l2(g, q, qi, ni)
+    want = np.array([po.l2_wave(q[a], base[b]) for a, b in zip(qi, ni)], np.float32)
+    assert got.tobytes() == want.tobytes()
+    exact = ((q[qi].astype(np.float64) - base[ni].astype(np.float64)) ** 2).sum(1)
+    assert np.all(np.abs(got - exact) <= 1e-5 * np.maximum(exact, 1e-30))
+    # integer-valued inputs: every partial sum is exact
+    bi = rng.integers(-8, 8, (n, dim)).astype(np.float32)
+    g2 = search.GPUGraph(bi, np.zeros((n, 4), np.uint32))
+    qi2 = rng.integers(-8, 8, (nq, dim)).astype(np.float32)
+    got2 = search.debug_l2(g2, qi2, qi, ni)
+    assert np.array_equal(got2, ((qi2[qi] - bi[ni]) ** 2).sum(1).astype(np.float32))
+
+
+def _keys(d, ids):
+    return search.make_keys(np.asarray(d, np.float32), np.asarray(ids))
+
+
+@pytest.mark.parametrize("topk,bsize", [(16, 16), (64, 32), (100, 32), (128, 64), (256, 64), (256, 128),
+                                        (512, 64), (512, 128)])
+def test_beam_merge_keeps_smallest(gpu, topk, bsize):
+    rng = np.random.default_rng(topk * 7 + bsize)
+    n = 4 * max(topk, bsize)
+    perm = rng.permutation(n)
+    keys = _keys(perm.astype(np.float32), perm)[: (n // bsize) * bsize].reshape(-1, bsize)
+    picked, beam = search.debug_beam(topk, keys, 0, 0)
+    opicked, obeam = po.beam_run(topk, keys, 0, 0)
+    assert np.array_equal(beam, obeam)
+    ids = ((beam >> np.uint64(1)) & np.uint64(0x7FFFFFFF)).astype(np.int64)
+    assert np.array_equal(ids[:topk], np.sort(perm[:keys.size])[:topk])
+
+
+@pytest.mark.parametrize("topk,bsize,picks", [(64, 32, 1), (128, 32, 2), (256, 64, 1), (512, 64, 3),
+                                              (100, 16, 2)])
+def test_beam_interleaved_pick_no_dup_and_order(gpu, topk, bsize, picks):
+    rng = np.random.default_rng(topk + picks)
+    n = 8 * topk
+    d = rng.permutation(n).astype(np.float32)
+    ids = rng.permutation(n)
+    keys = _keys(d, ids)
+    keys[rng.random(n) < 0.2] = np.uint64(po.EMPTY_KEY)  # idle lanes
+    keys = keys[: (n // bsize) * bsize].reshape(-1, bsize)
+    picked, beam = search.debug_beam(topk, keys, picks, 0)
+    opicked, obeam = po.beam_run(topk, keys, picks, 0)
+    assert np.array_equal(picked, opicked)
+    assert np.array_equal(beam, obeam)
+    p = picked.ravel()
+    p = p[p != po.INVALID_ID]
+    assert len(set(p.tolist())) == len(p) > 0
+
+
+def test_beam_ties_and_run_rule(gpu):
+    rng = np.random.default_rng(11)
+    # many equal distances, distinct ids: ties are ordered by id
+    d = rng.integers(0, 6, 512).astype(np.float32)
+    keys = _keys(d, rng.permutation(512)).reshape(-1, 64)
+    picked, beam = search.debug_beam(128, keys, 2, 0)
+    opicked, obeam = po.beam_run(128, keys, 2, 0)
+    assert np.array_equal(picked, opicked)
+    assert np.array_equal(beam, obeam)
+    # duplicated (dist, id) pairs (the rabitq beam): the run rule
+    keys = _keys(d, rng.integers(0, 40, 512)).reshape(-1, 64)
+    picked, beam = search.debug_beam(128, keys, 2, 1)
+    opicked, obeam = po.beam_run(128, keys, 2, 1)
+    assert np.array_equal(picked, opicked)
+    assert np.array_equal(beam, obeam)
+
+
+@pytest.mark.parametrize("n", [1, 5, 64, 100, 128, 200, 256, 300, 512])
+def test_bitonic_sort(gpu, n):
+    rng = np.random.default_rng(n)
+    keys = rng.integers(0, 2**63, n, dtype=np.uint64)
+    keys[: n // 3] = keys[0]
+    assert np.array_equal(search.debug_sort(keys), np.sort(keys))
+
+
+@pytest.mark.parametrize("bloom,cap", [(0, 32), (0, 64), (0, 1024), (0, 4096), (1, 256), (1, 1024), (1, 8192)])
+def test_filters_match_oracle(gpu, bloom, cap):
+    rng = np.random.default_rng(cap + bloom)
+    nb = (cap // 32 + 4) if not bloom else 40
+    keys = rng.integers(0, 3 * cap, (nb, 64)).astype(np.uint32)
+    keys[:, 50:] = 0xFFFFFFFF
+    keys[1, 7] = keys[1, 2]
+    keys[2, 9] = keys[1, 4]
+    qk = rng.integers(0, 3 * cap, 500).astype(np.uint32)
+    new, cont = search.debug_filter(bloom, cap, keys, qk)
+    onew, ocont = po.filter_run(bloom, cap, keys, qk)
+    assert np.array_equal(new, onew)
+    assert np.array_equal(cont, ocont)
+
+
+def test_host_tools_do_not_need_the_gpu_but_index_does(gpu):
+    base = host.gen_normalized(64, 8, 1)
+    with pytest.raises(ValueError):
+        search.GPUGraph(base, np.full((64, 4), 64, np.uint32))  # edge out of range

@@ -1,0 +1,151 @@
+"""The GPU-semantics oracle (the model the HIP kernels are compared with) against the
+reference-pinned CPU-reference oracle and closed forms."""
+import numpy as np
+import pytest
+
+from oracle import pyoracle as po
+
+
+def _idx(arrays):
+    return po.OracleIndex(arrays["base"], arrays["edges"], arrays["codes"], arrays["factors"], arrays["signs"])
+
+
+@pytest.mark.parametrize("name", ["d32", "d100"])
+@pytest.mark.parametrize("l2", [po.L2_SEQ, po.L2_WAVE])
+def test_base_hash_reduces_to_cpuref_without_forgetting(golden_sets, name, l2):
+    """gpu_search_base with a table that never overflows and never resets is the CPU
+    reference search (cpu_search_base.hpp) exactly."""
+    arrays, _ = golden_sets[name]
+    oi = _idx(arrays)
+    ep = int(arrays["entry"])
+    for topk in (16, 64, 128):
+        a, da, sa = oi.search(arrays["queries"], 10, po.BASE_HASH, topk, ep, 1024, 65536, 0, l2)
+        b, db, sb = oi.search(arrays["queries"], 10, po.BASE_CPUREF, topk, ep, 1024, 65536, 0, l2)
+        assert np.array_equal(a, b)
+        assert np.array_equal(da, db)
+        assert np.array_equal(sa[:, 1:3], sb[:, 1:3])  # expansions, distance evaluations
+
+
+@pytest.mark.parametrize("name", ["d32", "d100"])
+def test_bloom_without_false_positives_equals_hash(golden_sets, name):
+    """With 2^22 Bloom bits no false positive occurs for a few thousand keys, so bwarp
+    reduces to warp (same resets, same candidates)."""
+    arrays, _ = golden_sets[name]
+    oi = _idx(arrays)
+    ep = int(arrays["entry"])
+    for reset in (0, 4, 16):
+        a, _, _ = oi.search(arrays["queries"], 10, po.BASE_HASH, 64, ep, 1024, 65536, reset)
+        b, _, _ = oi.search(arrays["queries"], 10, po.BASE_BLOOM, 64, ep, 1024, 1 << 22, reset)
+        assert np.array_equal(a, b)
+
+
+def test_forgettable_reset_properties(golden_sets):
+    arrays, _ = golden_sets["d32"]
+    oi = _idx(arrays)
+    ep = int(arrays["entry"])
+    q = arrays["queries"]
+    base = arrays["base"]
+    r0, _, _ = oi.search(q, 10, po.BASE_CPUREF, 64, ep, 1024, 1024, 0)
+    for reset in (1, 2, 16):
+        ids, d, st = oi.search(q, 10, po.BASE_HASH, 64, ep, 1024, 1024, reset)
+        # each returned distance is the L2 of the returned node; ascending; distinct
+        for i in range(q.shape[0]):
+            for j in range(10):
+                assert d[i, j] == np.float32(po.l2_wave(q[i], base[ids[i, j]]))
+            assert np.all(np.diff(d[i]) >= 0)
+            assert len(set(ids[i].tolist())) == 10
+        # forgetting only re-admits nodes, so recall stays in the same range
+        gt = arrays["gt"]
+        assert po.recall(ids, gt)[0] >= po.recall(r0, gt)[0] - 0.02
+
+
+def test_small_filter_overflow_is_deterministic(golden_sets):
+    arrays, _ = golden_sets["d32"]
+    oi = _idx(arrays)
+    ep = int(arrays["entry"])
+    a = oi.search(arrays["queries"], 10, po.BASE_HASH, 64, ep, 1024, 32, 64)
+    b = oi.search(arrays["queries"], 10, po.BASE_HASH, 64, ep, 1024, 32, 64)
+    assert np.array_equal(a[0], b[0])
+
+
+@pytest.mark.parametrize("name", ["d32", "d100"])
+def test_rabitq_gpu_semantics_properties(golden_sets, name):
+    arrays, _ = golden_sets[name]
+    oi = _idx(arrays)
+    ep = int(arrays["entry_rabitq"])
+    q, base, gt = arrays["queries"], arrays["base"], arrays["gt"]
+    for topk in (32, 64):
+        ids, d, st = oi.search(q, 10, po.RABITQ_GPU, topk, ep, 1024, 1024, 0)
+        cids, _, _ = oi.search(q, 10, po.RABITQ_CPUREF, topk, ep, 1024, 1024, 0, po.L2_SEQ)
+        for i in range(q.shape[0]):
+            valid = ids[i] != po.INVALID_ID
+            # exact-L2 rerank, ascending, deduplicated
+            for j in np.nonzero(valid)[0]:
+                assert d[i, j] == np.float32(po.l2_wave(q[i], base[ids[i, j]]))
+            assert np.all(np.diff(d[i][valid]) >= 0)
+            assert len(set(ids[i][valid].tolist())) == int(valid.sum())
+        assert np.all(st[:, 4] > 0)  # rerank evaluations
+        # different estimator (dither) and visited rule than the CPU reference: recall only
+        assert abs(po.recall(ids, gt)[0] - po.recall(cids, gt)[0]) < 0.1
+
+
+def test_beam_closed_forms():
+    """topk_*_merge tests: shuffled 0..n-1 keep exactly the topk smallest; no_dup: picks
+    never repeat; pick order is ascending (test_topk_reg_pick_order.cu)."""
+    rng = np.random.default_rng(200)
+    for topk, bsize in [(64, 32), (128, 64), (256, 64), (100, 32), (512, 128)]:
+        n = 4 * topk
+        perm = rng.permutation(n)
+        keys = make(perm.astype(np.float32), perm)
+        keys = keys[: (n // bsize) * bsize].reshape(-1, bsize)
+        picked, beam = po.beam_run(topk, keys, 0, 0)
+        ids = ((beam >> np.uint64(1)) & np.uint64(0x7FFFFFFF)).astype(np.int64)
+        kept = np.sort(perm[: keys.size])[:topk]
+        assert np.array_equal(ids[:len(kept)], kept)
+        picked, beam = po.beam_run(topk, keys, 2, 0)
+        p = picked.ravel()
+        p = p[p != po.INVALID_ID]
+        assert len(set(p.tolist())) == len(p)
+
+
+def test_pick_run_rule_keeps_beam_sorted():
+    k = make(np.array([1, 1, 1, 2], np.float32), np.array([5, 5, 5, 6]))
+    keys = np.concatenate([k, np.full(4, po.EMPTY_KEY, np.uint64)]).reshape(1, 8)
+    picked, beam = po.beam_run(64, keys, 3, 1)
+    assert picked[0].tolist() == [5, 5, 5]
+    assert np.all(np.diff(beam[:4].astype(object)) >= 0)
+    assert [int(b) & 1 for b in beam[:4]] == [1, 1, 1, 0]
+
+
+def test_filters_against_sets():
+    rng = np.random.default_rng(3)
+    for cap in (64, 512, 1024):
+        keys = rng.integers(0, 5000, (cap // 64 + 2, 64)).astype(np.uint32)
+        keys[0, 5] = keys[0, 3]  # duplicate inside one batch
+        keys[:, 60:] = po.INVALID_ID
+        qk = rng.integers(0, 5000, 300).astype(np.uint32)
+        new, cont = po.filter_run(False, cap, keys, qk)
+        seen = set()
+        size = 1 << int(np.ceil(np.log2(cap)))
+        for b in range(keys.shape[0]):
+            for l in range(64):
+                k = int(keys[b, l])
+                if k == po.INVALID_ID:
+                    assert new[b, l] == 0
+                    continue
+                exp = int(k not in seen and len(seen) < size)
+                assert new[b, l] == exp
+                if exp:
+                    seen.add(k)
+        assert cont.tolist() == [int(int(k) in seen) for k in qk]
+        # bloom: never a false negative; duplicates inside a batch are new once
+        newb, contb = po.filter_run(True, cap * 8, keys, qk)
+        inserted = {int(k) for k in keys.ravel() if k != po.INVALID_ID}
+        assert all(contb[i] for i, k in enumerate(qk) if int(k) in inserted)
+        assert not (newb[0, 5] and newb[0, 3])
+
+
+def make(d, ids):
+    b = np.asarray(d, np.float32).view(np.uint32).astype(np.uint64)
+    o = np.where((b & 0x80000000) != 0, (~b) & 0xFFFFFFFF, b | 0x80000000)
+    return (o << np.uint64(32)) | (np.asarray(ids, np.uint64) << np.uint64(1))
