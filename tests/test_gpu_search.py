@@ -142,9 +142,17 @@ def test_recall_parity_with_cpu_reference(gpu):
     for topk in (64, 128):
         cref, _, _ = ds["oi"].search(ds["q"], 10, po.BASE_CPUREF, topk, ds["entry"], 1024, 1024, 0, po.L2_SEQ)
         rc = host.recall(cref, gt)[0]
-        for m in ("base", "bwarp1"):
-            ids, _, _, _, _, _ = run_both(ds, m, 10, topk)
-            assert abs(host.recall(ids, gt)[0] - rc) <= 0.005 + 1e-9, (m, topk)
+        # hash filter with the reference's default reset; Bloom filter with the reference
+        # config rule reset_interval = filter_capacity / 128 (config/search/bwarp*_f8192.json)
+        for m, cap, reset in (("base", 1024, 16), ("warp2", 1024, 16), ("bwarp1", 8192, 64)):
+            ids, _, _, _, _, _ = run_both(ds, m, 10, topk, cap=cap, reset=reset)
+            rg = host.recall(ids, gt)[0]
+            print(f"topk={topk} {m}: gpu {rg:.4f} cpu_cli {rc:.4f}")
+            assert abs(rg - rc) <= 0.005 + 1e-9, (m, topk, rg, rc)
         qref, _, _ = ds["oi"].search(ds["q"], 10, po.RABITQ_CPUREF, topk, ds["erq"], 1024, 1024, 0, po.L2_SEQ)
         ids, _, _, _, _, _ = run_both(ds, "rabitq", 10, topk)
-        assert abs(host.recall(ids, gt)[0] - host.recall(qref, gt)[0]) <= 0.02, topk
+        rg, rq = host.recall(ids, gt)[0], host.recall(qref, gt)[0]
+        print(f"topk={topk} rabitq: gpu {rg:.4f} cpu_cli {rq:.4f}")
+        # the GPU estimator (dithered quantizer, expanded-set re-entry) is not the CPU one
+        # (gpu_search_rabitq.cuh vs cpu_search_rabitq.hpp): it may only be better
+        assert rg >= rq - 0.005, (topk, rg, rq)
