@@ -1,0 +1,157 @@
+// gpu_cli: the reference's GPU search CLI (src/gpu_cli.cu:353-492) on the MI355X.
+//
+// Reads one JSON object from stdin:
+//   {"data":   {"graph", "base", "query", "gt", "codebook"?},
+//    "search": {"mode", "K", "topk_size", "filter_capacity", "max_iterations", "reset_interval"}}
+// loads the files, uploads the index through the C-ABI (include/bs_hip.h), runs one
+// warm-up and 5 timed searches and prints the reference's line protocol:
+//   data: N points, dim=D, degree=R, queries=Q, entry=E
+//   search: mode=M K=K
+//     time: X ms  qps: Y            (kernel time per run, HIP events)
+//     duplicates: ...               (only when some query returned an id twice)
+//   recall@K: R
+// Exit status 1 on a configuration or input error, with the message on stderr.
+#include "bs_hip.h"
+#include "bs_host.h"
+#include "json_lite.hpp"
+
+#include <cstdint>
+#include <cstdio>
+#include <cstdlib>
+#include <iostream>
+#include <iterator>
+#include <string>
+#include <vector>
+
+namespace {
+
+struct Buf {
+    void* p = nullptr;
+    ~Buf() { bs_host_free(p); }
+};
+
+int die(const std::string& m) {
+    std::cerr << m << std::endl;
+    return 1;
+}
+
+}  // namespace
+
+int main() {
+    const std::string text((std::istreambuf_iterator<char>(std::cin)), std::istreambuf_iterator<char>());
+    jsonl::Value j;
+    try {
+        j = jsonl::parse(text);
+    } catch (const std::exception& e) {
+        return die(std::string("JSON parse error: ") + e.what());
+    }
+    try {
+        if (j.has("search") && j.at("search").has("mode")) {
+            const std::string mode = j.at("search").at("mode").as_string();
+            if (mode.rfind("sophia_", 0) == 0)
+                return die("mode " + mode + ": the legacy sophia_* stack is not part of this build");
+        }
+        if (!j.has("data")) return die("Missing \"data\" key");
+        const jsonl::Value& jd = j.at("data");
+        const std::string graph_file = jd.at("graph").as_string(), base_file = jd.at("base").as_string(),
+                          query_file = jd.at("query").as_string(), gt_file = jd.at("gt").as_string(),
+                          codebook_file = jd.value("codebook", std::string());
+
+        Buf eb, vb, qb, gb;
+        uint64_t n = 0, nv = 0, nq = 0, ngt = 0;
+        uint32_t degree = 0, dim = 0, qdim = 0, gt_k = 0;
+        if (bs_read_graph(graph_file.c_str(), reinterpret_cast<uint32_t**>(&eb.p), &n, &degree))
+            return die(bs_host_last_error());
+        std::cout << "Loaded graph: " << n << " nodes, degree " << degree << " from " << graph_file << "\n";
+        if (bs_read_vecs(base_file.c_str(), 0, &vb.p, &nv, &dim)) return die(bs_host_last_error());
+        if (nv != n) return die("base vectors (" + std::to_string(nv) + ") do not match graph nodes (" +
+                                std::to_string(n) + ")");
+        std::cout << "Loaded vectors: " << n << " x " << dim << " from " << base_file << "\n";
+        if (bs_read_vecs(query_file.c_str(), 0, &qb.p, &nq, &qdim)) return die(bs_host_last_error());
+        if (qdim != dim && nq) return die("query dim does not match base dim");
+        if (bs_read_vecs(gt_file.c_str(), 1, &gb.p, &ngt, &gt_k)) return die(bs_host_last_error());
+        if (ngt < nq) return die("ground truth has fewer rows than queries");
+
+        const float* vecs = static_cast<const float*>(vb.p);
+        const uint32_t* edges = static_cast<const uint32_t*>(eb.p);
+        bs_index ix = nullptr;
+        if (bs_index_create(vecs, edges, n, dim, degree, &ix)) return die(bs_last_error());
+        const uint32_t entry = bs_entry_point(vecs, n, dim);
+        std::cout << "data: " << n << " points, dim=" << dim << ", degree=" << degree << ", queries=" << nq
+                  << ", entry=" << entry << std::endl;
+
+        if (!j.has("search")) return die("Missing \"search\" key");
+        const jsonl::Value& js = j.at("search");
+        const std::string mode = js.value("mode", std::string("base"));
+        const int K = static_cast<int>(js.value("K", 100.0));
+        std::cout << "search: mode=" << mode << " K=" << K << std::endl;
+        if (K <= 0) return die("K must be positive");
+
+        bs_search_cfg cfg{};
+        cfg.K = static_cast<uint32_t>(K);
+        cfg.topk_size = static_cast<uint32_t>(js.value("topk_size", 256.0));
+        cfg.filter_capacity = static_cast<uint32_t>(js.value("filter_capacity", 1024.0));
+        cfg.max_iterations = static_cast<int32_t>(js.value("max_iterations", 1024.0));
+        cfg.reset_interval = static_cast<int32_t>(js.value("reset_interval", 16.0));
+        cfg.entry_point = entry;
+        cfg.queries_per_group = 1;
+        if (mode == "rabitq") {
+            if (codebook_file.empty()) return die("rabitq mode requires \"codebook\" in data config");
+            uint32_t cb_entry = 0, pdim = 0;
+            Buf cb, fb, sb;
+            if (bs_read_codebook(codebook_file.c_str(), n, dim, degree, &cb_entry,
+                                 reinterpret_cast<uint32_t**>(&cb.p), reinterpret_cast<float**>(&fb.p),
+                                 reinterpret_cast<float**>(&sb.p), &pdim))
+                return die(bs_host_last_error());
+            std::cout << "Loaded rabitq codebook: " << n << " nodes, dim=" << dim << ", degree=" << degree
+                      << ", padded_dim=" << pdim << " (entry=" << cb_entry << ")\n";
+            if (bs_index_attach_rabitq(ix, static_cast<uint32_t*>(cb.p), static_cast<float*>(fb.p),
+                                       static_cast<float*>(sb.p), pdim))
+                return die(bs_last_error());
+            cfg.mode = BS_RABITQ;
+            cfg.entry_point = (cb_entry != 0xFFFFFFFFu) ? cb_entry : entry;
+            cfg.reset_interval = 0;
+        } else {
+            if (cfg.topk_size < static_cast<uint32_t>(K))
+                return die("topk_size (" + std::to_string(cfg.topk_size) + ") must be >= K (" + std::to_string(K) + ")");
+            if (mode == "base") {
+                cfg.mode = BS_BASE;
+            } else if (mode.size() >= 5 && (mode.rfind("warp", 0) == 0 || mode.rfind("bwarp", 0) == 0)) {
+                const bool bloom = mode[0] == 'b';
+                const std::string ny = mode.substr(bloom ? 5 : 4);
+                if (ny != "1" && ny != "2" && ny != "4" && ny != "8") return die("Unknown mode: " + mode);
+                cfg.mode = bloom ? BS_GROUP_BLOOM : BS_GROUP;
+                cfg.queries_per_group = static_cast<uint32_t>(std::atoi(ny.c_str()));
+            } else {
+                return die("Unknown mode: " + mode);
+            }
+        }
+
+        const float* queries = static_cast<const float*>(qb.p);
+        std::vector<uint32_t> results(nq * static_cast<uint64_t>(K), 0xFFFFFFFFu);
+        bs_stats st{};
+        // one warm-up (the reference has none, so its first run includes launch set-up)
+        if (bs_search(ix, &cfg, queries, nq, results.data(), nullptr, &st)) return die(bs_last_error());
+        constexpr int NRUNS = 5;
+        double kms = 0.0;
+        for (int r = 0; r < NRUNS; ++r) {
+            if (bs_search(ix, &cfg, queries, nq, results.data(), nullptr, &st)) return die(bs_last_error());
+            kms += st.kernel_ms;
+        }
+        const double ms = kms / NRUNS;
+        std::cout << "  time: " << ms << " ms  qps: " << (ms > 0 ? nq / (ms / 1000.0) : 0.0) << std::endl;
+
+        // recall (src/gpu_cli.cu:28-51): reads gt_k columns per query
+        std::vector<int32_t> gt(static_cast<const int32_t*>(gb.p), static_cast<const int32_t*>(gb.p) + nq * gt_k);
+        uint64_t dups = 0;
+        const double rec = nq ? bs_recall(results.data(), nq, static_cast<uint32_t>(K), gt.data(), gt_k, &dups) : 0.0;
+        if (dups > 0)
+            std::cout << "  duplicates: " << dups << " total (" << static_cast<double>(dups) / nq << " avg/query)"
+                      << std::endl;
+        std::cout << "recall@" << K << ": " << rec << std::endl;
+        bs_index_destroy(ix);
+        return 0;
+    } catch (const std::exception& e) {
+        return die(e.what());
+    }
+}

@@ -237,6 +237,7 @@ extern "C" int bs_build_vamana(const float* vecs, uint64_t n, uint32_t dim, uint
     for (auto& s : scr) s.stamp.assign(n, 0);
 
     uint64_t start = 1;
+    double last_print = 0.0;
     while (start < n) {
         const uint64_t end = std::min(std::min(start * 2, start + batch_bound), n);
 #pragma omp parallel for schedule(dynamic, 1) num_threads(T)
@@ -286,8 +287,11 @@ extern "C" int bs_build_vamana(const float* vecs, uint64_t n, uint32_t dim, uint
         }
         if (verbose) {
             const double el = std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count();
-            std::fprintf(stderr, "  build_graph: batch [%llu, %llu) done, %.1fs\n",
-                         static_cast<unsigned long long>(start), static_cast<unsigned long long>(end), el);
+            if (end == n || el - last_print >= 5.0) {
+                std::fprintf(stderr, "  build_graph: %llu / %llu points inserted, %.1fs\n",
+                             static_cast<unsigned long long>(end), static_cast<unsigned long long>(n), el);
+                last_print = el;
+            }
         }
         start = end;
     }

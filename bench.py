@@ -51,6 +51,8 @@ def parse():
     ap.add_argument("--cpu-procs", type=int, default=0)
     ap.add_argument("--cpu-queries", type=int, default=400, help="queries per CPU process")
     ap.add_argument("--sweep", default="", help="comma list of topk values to sweep (extra lines on stderr)")
+    ap.add_argument("--calib-copy-mib", type=int, default=0,
+                    help="run one elementwise copy of this many MiB first (HBM-counter calibration under rocprofv3)")
     return ap.parse_args()
 
 
@@ -142,6 +144,26 @@ def cpu_baseline(files, nq_total, args, entry_line_check=None):
             "sample": f"{per} queries, CPU oracle restatement of cpu_search_base.hpp, one thread"}
 
 
+def kernel_name(args):
+    tr = 1 if args.topk <= 64 else 2 if args.topk <= 128 else 4 if args.topk <= 256 else 8
+    cr = 1 if args.degree <= 64 else 2
+    qm = 1 if (args.dim + 3) // 4 <= 64 else 4
+    mode = {"base": 0, "bwarp": 1, "rabitq": 2}.get(args.mode.rstrip("0123456789"), 0)
+    return f"bsd::search_kernel<{tr}, {cr}, {qm}, {mode}>"
+
+
+def measured_traffic(args):
+    """HBM bytes per launch of the search kernel from the committed rocprofv3 --pmc summary
+    (FETCH_SIZE / WRITE_SIZE scaled by a 1 GiB copy), for the default workload only."""
+    default = (args.n, args.nq, args.dim, args.degree, args.mode, args.topk, args.K, args.cap, args.reset) == \
+        (1_000_000, 10_000, 128, 32, "base", 256, 100, 1024, 16)
+    path = os.path.join(ROOT, "profiles", "search_kernel_base_1Mx128_traffic.json")
+    if not default or not os.path.exists(path):
+        return None
+    with open(path) as f:
+        return json.load(f)["traffic_bytes"]
+
+
 def _has_taskset():
     from shutil import which
     return which("taskset") is not None
@@ -150,8 +172,9 @@ def _has_taskset():
 def main():
     args = parse()
     if args.gpus != 1:
-        print(f"bench.py: this build measures one GPU only (--gpus {args.gpus} requested); the path shards "
-              "by queries with no exchange between GPUs (see DESIGN.md)", file=sys.stderr)
+        print(f"bench.py: this build measures one GPU only (--gpus {args.gpus} requested); the search shards "
+              "by queries (independent units, no exchange between GPUs), so N GPUs run N disjoint query "
+              "shards of the same replicated index", file=sys.stderr)
         sys.exit(2)
     import numpy as np
     import torch
@@ -174,6 +197,15 @@ def main():
     torch.cuda.empty_cache()
     log(f"ground truth top-100: {time.time() - t1:.1f}s")
     entry = host.entry_point(base)
+    if args.calib_copy_mib:
+        # a plain read-once/write-once kernel of known size: rocprofv3 --pmc FETCH_SIZE /
+        # WRITE_SIZE on it gives the counter-to-bytes factor used for the search kernel
+        x = torch.ones(args.calib_copy_mib << 18, dtype=torch.float32, device=dev)
+        y = torch.empty_like(x)
+        torch.add(x, 1.0, out=y)
+        torch.cuda.synchronize()
+        log(f"calibration copy: {args.calib_copy_mib} MiB read + {args.calib_copy_mib} MiB written")
+        del x, y
     g = search.GPUGraph(base, edges)
     cfg = search.GPUBaseSearchCfg(args.topk, args.cap, entry, args.max_it, args.reset)
     nq, K = args.nq, args.K
@@ -241,6 +273,7 @@ def main():
         os.rmdir(tmp)
         log(f"cpu baseline: {cpu} ({time.time() - t1:.1f}s)")
 
+    traffic = measured_traffic(args)
     out = {
         "metric": "QPS @ recall@10>=0.95, 1Mx128 fp32, 1 MI355X; achieved HBM GB/s",
         "value": round(qps, 1),
@@ -261,8 +294,8 @@ def main():
                    "recall_at_10": round(r_10, 4), f"recall_at_{K}": round(r_k, 4), "duplicates": dups,
                    "expansions_per_query": round(E / nq, 2), "dist_evals_per_query": round(D / nq, 2)},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "bsd::search_kernel<4,1,1,0> (base, hash)", "avg_launch_ms": round(avg_kernel_ms, 3),
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
+                     "kernel": kernel_name(args), "avg_launch_ms": round(avg_kernel_ms, 3),
                      "bytes_per_launch": bytes_launch},
         "cpu_baseline": cpu,
     }
