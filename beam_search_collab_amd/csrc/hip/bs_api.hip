@@ -33,17 +33,6 @@ uint32_t log2_ceil(uint32_t v) {
     return b;
 }
 
-bsd::L2Shape l2_shape(uint32_t dim) {
-    bsd::L2Shape L;
-    L.chunks = (dim + 3) / 4;
-    L.G = 1;
-    while (L.G < L.chunks && L.G < 64) L.G <<= 1;
-    L.gshift = log2_ceil(L.G);
-    L.QR = (L.chunks + L.G - 1) / L.G;
-    L.rpp = 64 / L.G;
-    return L;
-}
-
 int check_device() {
     int dev = 0;
     HIP_TRY(hipGetDevice(&dev));
@@ -240,8 +229,8 @@ int make_plan(bs_index ix, const bs_search_cfg* cfg, uint64_t nq, Plan& pl) {
     pl.mode = mode;
     pl.TR = T <= 64 ? 1 : T <= 128 ? 2 : T <= 256 ? 4 : 8;
     pl.CR = ix->degree <= 64 ? 1 : 2;
-    bsd::L2Shape L = l2_shape(ix->dim);
-    pl.QMAX = L.QR <= 1 ? 1 : 4;
+    bsd::L2Shape L = bsd::l2_shape(ix->dim);
+    pl.QMAX = 4;
     if (L.QR > 4) return fail(BS_EINVAL, "dim too large");
 
     bsd::SearchParams& p = pl.p;

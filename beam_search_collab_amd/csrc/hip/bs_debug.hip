@@ -49,17 +49,6 @@ int dfail(int code, const std::string& msg) {
     return code;
 }
 
-bsd::L2Shape shape_of(uint32_t dim) {
-    bsd::L2Shape L;
-    L.chunks = (dim + 3) / 4;
-    L.G = 1;
-    while (L.G < L.chunks && L.G < 64) L.G <<= 1;
-    L.gshift = 0;
-    while ((1u << L.gshift) < L.G) ++L.gshift;
-    L.QR = (L.chunks + L.G - 1) / L.G;
-    L.rpp = 64 / L.G;
-    return L;
-}
 }  // namespace
 
 // ---------------------------------------------------------------------------
@@ -99,14 +88,10 @@ extern "C" int bs_debug_l2(bs_index idx, const float* queries, uint64_t nq, cons
     DTRY(hipMemcpy(dq.p, queries, nq * dim * 4, hipMemcpyHostToDevice));
     DTRY(hipMemcpy(dqi.p, qi, npairs * 4, hipMemcpyHostToDevice));
     DTRY(hipMemcpy(dni.p, ni, npairs * 4, hipMemcpyHostToDevice));
-    const bsd::L2Shape L = shape_of(dim);
+    const bsd::L2Shape L = bsd::l2_shape(dim);
     const dim3 grid(static_cast<uint32_t>((npairs + 3) / 4)), block(256);
-    if (L.QR <= 1)
-        hipLaunchKernelGGL(dbg_l2_kernel<1>, grid, block, 0, nullptr, vecs, dstride, dq.p, dim, dqi.p, dni.p, npairs, L,
-                           dout.p);
-    else
-        hipLaunchKernelGGL(dbg_l2_kernel<4>, grid, block, 0, nullptr, vecs, dstride, dq.p, dim, dqi.p, dni.p, npairs, L,
-                           dout.p);
+    hipLaunchKernelGGL(dbg_l2_kernel<4>, grid, block, 0, nullptr, vecs, dstride, dq.p, dim, dqi.p, dni.p, npairs, L,
+                       dout.p);
     DTRY(hipGetLastError());
     DTRY(hipMemcpy(out, dout.p, npairs * 4, hipMemcpyDeviceToHost));
     return BS_OK;

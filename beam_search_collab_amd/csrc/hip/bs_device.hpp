@@ -57,9 +57,25 @@ __device__ __forceinline__ uint32_t key_id(uint64_t k) { return static_cast<uint
 // ---------------------------------------------------------------------------
 template <int TR, int CR>
 __device__ __forceinline__ void beam_merge(uint64_t (&beam)[TR], const uint64_t (&ck)[CR],
-                                           const uint64_t (&cmask)[CR], uint32_t T,
+                                           const uint64_t (&cmask_in)[CR], uint32_t T,
                                            uint64_t* lds_scratch) {
     const uint32_t lane = lane_id();
+    // A candidate whose key is >= the beam's last key (EMPTY while the beam is not full)
+    // lands at position >= T and is evicted (ties go after beam entries), so it is dropped
+    // before the rank loop; the merged beam is the same.
+    uint64_t thr = EMPTY_KEY;
+    const uint32_t lr = (T - 1) >> 6, ll = (T - 1) & 63u;
+#pragma unroll
+    for (int r = 0; r < TR; ++r)
+        if (static_cast<uint32_t>(r) == lr) thr = readlane64(beam[r], ll);
+    uint64_t cmask[CR];
+    bool any = false;
+#pragma unroll
+    for (int rc = 0; rc < CR; ++rc) {
+        cmask[rc] = cmask_in[rc] & ballot(ck[rc] < thr);
+        any = any || cmask[rc] != 0;
+    }
+    if (!any) return;
     uint32_t bpos[TR];
 #pragma unroll
     for (int r = 0; r < TR; ++r) bpos[r] = static_cast<uint32_t>(r) * 64u + lane;
@@ -384,6 +400,24 @@ struct L2Shape {
     uint32_t G, gshift, QR, chunks, rpp;  // rpp = rows per pass = 64 / G
 };
 
+// Row layout for `dim`: chunks = dim/4 float4 chunks; G = pow2ceil(chunks)/4 lanes per row
+// (1 <= G <= 64), so each lane holds QR = ceil(chunks/G) <= 4 chunks (for dim <= 1024) and a
+// 64-lane pass covers 64/G rows.  Four chunks per lane keep the butterfly short (log2 G
+// steps per pass) and put 64/G rows of loads in flight per pass.
+__host__ __device__ inline L2Shape l2_shape(uint32_t dim) {
+    L2Shape L;
+    L.chunks = (dim + 3) / 4;
+    uint32_t p = 1;
+    while (p < L.chunks) p <<= 1;
+    L.G = p >= 4 ? p / 4 : 1;
+    if (L.G > 64) L.G = 64;
+    L.gshift = 0;
+    while ((1u << L.gshift) < L.G) ++L.gshift;
+    L.QR = (L.chunks + L.G - 1) / L.G;
+    L.rpp = 64 / L.G;
+    return L;
+}
+
 template <int QMAX>
 __device__ __forceinline__ float l2_partial(const float4 (&q)[QMAX], const float* row, uint32_t lig,
                                             const L2Shape& L, bool active) {
@@ -429,7 +463,10 @@ template <int QMAX>
 __device__ __forceinline__ void l2_rows(const float4 (&q)[QMAX], const float* base, uint64_t stride,
                                         const uint32_t* lds_ids, float* lds_d, uint32_t cnt,
                                         const L2Shape& L) {
-    constexpr int PB = 4;
+#ifndef BS_L2_PASSES_IN_FLIGHT
+#define BS_L2_PASSES_IN_FLIGHT 2
+#endif
+    constexpr int PB = BS_L2_PASSES_IN_FLIGHT;
     const uint32_t lane = lane_id();
     const uint32_t g = lane >> L.gshift, lig = lane & (L.G - 1);
     for (uint32_t j0 = 0; j0 < cnt; j0 += PB * L.rpp) {

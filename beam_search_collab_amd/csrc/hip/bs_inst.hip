@@ -22,7 +22,8 @@ static hipError_t launch_one(const SearchParams& p, dim3 grid, dim3 block, size_
 
 template <int TR, int CR>
 static hipError_t launch_q(const SearchParams& p, int QMAX, dim3 g, dim3 b, size_t lds, hipStream_t s) {
-    return QMAX == 1 ? launch_one<TR, CR, 1>(p, g, b, lds, s) : launch_one<TR, CR, 4>(p, g, b, lds, s);
+    (void)QMAX;  // every dim <= 1024 fits 4 float4 chunks per lane (bsd::l2_shape)
+    return launch_one<TR, CR, 4>(p, g, b, lds, s);
 }
 
 template <int TR>

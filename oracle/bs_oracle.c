@@ -94,14 +94,16 @@ float orc_l2_seq(const float* a, const float* b, int dim) {
 /* The HIP kernels' L2 order (the reference's l2_warp, l2.cuh:26-40, is a lane-strided
  * partial sum plus a shuffle tree; this build's wave64 form is restated here):
  * rows are zero-padded to dpad = roundup(dim, 4) floats = `chunks` float4 chunks; a row
- * is handled by G = min(64, pow2ceil(chunks)) lanes; lane l accumulates the chunks
- * j = l, l+G, l+2G, ... and within a chunk the 4 components in order, each with one
- * fused multiply-add p = fma(diff, diff, p); the G partials are then combined by an xor
- * butterfly p_l += p_{l^s}, s = 1, 2, 4, ..., G/2.  Padded components add exactly 0. */
+ * is handled by G = pow2ceil(chunks)/4 lanes (1 <= G <= 64); lane l accumulates the
+ * chunks j = l, l+G, l+2G, ... and within a chunk the 4 components in order, each with
+ * one fused multiply-add p = fma(diff, diff, p); the G partials are then combined by an
+ * xor butterfly p_l += p_{l^s}, s = 1, 2, 4, ..., G/2.  Padded components add exactly 0. */
 void orc_l2_wave_shape(int dim, int* group, int* per_lane) {
     int chunks = (dim + 3) / 4;
-    int g = 1;
-    while (g < chunks && g < 64) g <<= 1;
+    int p = 1;
+    while (p < chunks) p <<= 1;
+    int g = p >= 4 ? p / 4 : 1;
+    if (g > 64) g = 64;
     *group = g;
     *per_lane = (chunks + g - 1) / g;
 }
