@@ -418,26 +418,43 @@ __host__ __device__ inline L2Shape l2_shape(uint32_t dim) {
     return L;
 }
 
-template <int QMAX>
-__device__ __forceinline__ float l2_partial(const float4 (&q)[QMAX], const float* row, uint32_t lig,
-                                            const L2Shape& L, bool active) {
-    float p = 0.0f;
-    if (active) {
-        const float4* r4 = reinterpret_cast<const float4*>(row);
+// Partial sums of PB rows (one row per lane group per pass).  Every load is issued
+// unconditionally -- chunks outside the row are redirected to chunk 0 of the same row and
+// their difference is zeroed -- so all PB*QMAX loads of a lane are in flight together
+// (a conditional load would be followed by its own wait before the next one issues).
+// rows[t] must point at a valid row for every lane (inactive lane groups pass row 0).
+template <int QMAX, int PB>
+__device__ __forceinline__ void l2_partials(const float4 (&q)[QMAX], const float* const (&rows)[PB], uint32_t lig,
+                                            const L2Shape& L, float (&p)[PB]) {
+    float4 v[PB][QMAX];
+#pragma unroll
+    for (int t = 0; t < PB; ++t) {
+        const float4* r4 = reinterpret_cast<const float4*>(rows[t]);
 #pragma unroll
         for (int kk = 0; kk < QMAX; ++kk) {
             const uint32_t j = lig + static_cast<uint32_t>(kk) * L.G;
-            if (static_cast<uint32_t>(kk) < L.QR && j < L.chunks) {
-                const float4 v = r4[j];
-                const float d0 = q[kk].x - v.x, d1 = q[kk].y - v.y, d2 = q[kk].z - v.z, d3 = q[kk].w - v.w;
-                p = __builtin_fmaf(d0, d0, p);
-                p = __builtin_fmaf(d1, d1, p);
-                p = __builtin_fmaf(d2, d2, p);
-                p = __builtin_fmaf(d3, d3, p);
-            }
+            const bool ok = static_cast<uint32_t>(kk) < L.QR && j < L.chunks;
+            v[t][kk] = r4[ok ? j : 0u];
         }
     }
-    return p;
+    const bool full = L.QR * L.G == L.chunks && L.QR == static_cast<uint32_t>(QMAX);
+#pragma unroll
+    for (int t = 0; t < PB; ++t) {
+        float acc = 0.0f;
+#pragma unroll
+        for (int kk = 0; kk < QMAX; ++kk) {
+            const uint32_t j = lig + static_cast<uint32_t>(kk) * L.G;
+            const bool ok = full || (static_cast<uint32_t>(kk) < L.QR && j < L.chunks);
+            float d0 = q[kk].x - v[t][kk].x, d1 = q[kk].y - v[t][kk].y, d2 = q[kk].z - v[t][kk].z,
+                  d3 = q[kk].w - v[t][kk].w;
+            if (!ok) d0 = d1 = d2 = d3 = 0.0f;
+            acc = __builtin_fmaf(d0, d0, acc);
+            acc = __builtin_fmaf(d1, d1, acc);
+            acc = __builtin_fmaf(d2, d2, acc);
+            acc = __builtin_fmaf(d3, d3, acc);
+        }
+        p[t] = acc;
+    }
 }
 
 // query chunks of this lane: chunk j = lig + k*G, components beyond dim are 0
@@ -470,14 +487,15 @@ __device__ __forceinline__ void l2_rows(const float4 (&q)[QMAX], const float* ba
     const uint32_t lane = lane_id();
     const uint32_t g = lane >> L.gshift, lig = lane & (L.G - 1);
     for (uint32_t j0 = 0; j0 < cnt; j0 += PB * L.rpp) {
-        float p[PB];
+        const float* rows[PB];
 #pragma unroll
         for (int t = 0; t < PB; ++t) {
             const uint32_t j = j0 + static_cast<uint32_t>(t) * L.rpp + g;
-            const bool act = j < cnt;
-            const uint32_t id = act ? lds_ids[j] : 0u;
-            p[t] = l2_partial<QMAX>(q, base + static_cast<uint64_t>(id) * stride, lig, L, act);
+            const uint32_t id = (j < cnt) ? lds_ids[j] : 0u;
+            rows[t] = base + static_cast<uint64_t>(id) * stride;
         }
+        float p[PB];
+        l2_partials<QMAX, PB>(q, rows, lig, L, p);
 #pragma unroll
         for (int t = 0; t < PB; ++t) {
             const float s = bsw::group_sum(p[t], L.G);
@@ -491,11 +509,12 @@ __device__ __forceinline__ void l2_rows(const float4 (&q)[QMAX], const float* ba
 // L2 of one row, result in every lane
 template <int QMAX>
 __device__ __forceinline__ float l2_one(const float4 (&q)[QMAX], const float* row, const L2Shape& L) {
-    const uint32_t lane = lane_id();
-    const uint32_t g = lane >> L.gshift, lig = lane & (L.G - 1);
-    float p = l2_partial<QMAX>(q, row, lig, L, g == 0);
-    p = bsw::group_sum(p, L.G);
-    return __uint_as_float(readlane(__float_as_uint(p), 0));
+    const uint32_t lig = lane_id() & (L.G - 1);
+    const float* const rows[1] = {row};
+    float p[1];
+    l2_partials<QMAX, 1>(q, rows, lig, L, p);
+    const float r = bsw::group_sum(p[0], L.G);
+    return __uint_as_float(readlane(__float_as_uint(r), 0));
 }
 
 // ---------------------------------------------------------------------------
@@ -611,12 +630,16 @@ __device__ __forceinline__ void raw_sums(const uint32_t (&pl)[6], const uint32_t
     const uint32_t npass = (R + npp - 1) / npp;
     const uint32_t nl = lane / wpp, w = lane & (wpp - 1);
     for (uint32_t t0 = 0; t0 < npass; t0 += 4) {
-        uint32_t acc[4];
+        uint32_t acc[4], code[4];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {  // unconditional loads (index clamped) so all 4 are in flight
+            const uint32_t nb = (t0 + static_cast<uint32_t>(t)) * npp + nl;
+            code[t] = codes[(nb < R ? nb : 0u) * wpp + w];
+        }
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
             const uint32_t nb = (t0 + static_cast<uint32_t>(t)) * npp + nl;
-            const uint32_t code = (nb < R) ? codes[nb * wpp + w] : 0u;
-            acc[t] = raw_word(pl, code);
+            acc[t] = raw_word(pl, nb < R ? code[t] : 0u);
         }
 #pragma unroll
         for (int t = 0; t < 4; ++t) {

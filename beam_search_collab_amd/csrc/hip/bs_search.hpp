@@ -244,11 +244,12 @@ __global__ void __launch_bounds__(512) search_kernel(const SearchParams p) {
             for (int rc = 0; rc < CR; ++rc) {
                 const uint32_t i = static_cast<uint32_t>(rc) * 64u + lane;
                 uint64_t k = EMPTY_KEY;
-                if (valid[rc]) {
+                {
                     const float* fac = reinterpret_cast<const float*>(rec + p.rec_fac);
-                    const float est = estimate(rawbuf[i], qo.sum_q, qo.width, qo.low, fac[i], fac[p.R + i],
-                                               fac[2 * p.R + i], exact);
-                    k = make_key(est, child[rc]);
+                    const uint32_t ic = i < p.R ? i : 0u;  // unconditional loads, index clamped
+                    const float tx = fac[ic], fdq = fac[p.R + ic], fvq = fac[2 * p.R + ic];
+                    const float est = estimate(rawbuf[ic], qo.sum_q, qo.width, qo.low, tx, fdq, fvq, exact);
+                    if (valid[rc]) k = make_key(est, child[rc]);
                 }
                 ck[rc] = k;
                 cm[rc] = ballot(valid[rc]);
