@@ -134,7 +134,8 @@ extern "C" int bs_index_attach_rabitq(bs_index ix, const uint32_t* codes, const 
     if (padded_dim != p) return fail(BS_EINVAL, "padded_dim must be pow2ceil(dim) = " + std::to_string(p));
     if (padded_dim < 32 || padded_dim > 2048) return fail(BS_EINVAL, "padded_dim must be in 32..2048");
     const uint32_t R = ix->degree, wpp = padded_dim / 32;
-    uint32_t rw = ix->dstride + R + 3 * R + R * wpp;
+    const uint32_t cws = bsd::quad_shape(wpp, R).cws;  // code words per neighbour, >= 4
+    uint32_t rw = ix->dstride + R + 3 * R + R * cws;
     rw = (rw + 31) & ~31u;
     // assemble the records on the host in blocks and upload
     if (ix->d_recs) {
@@ -169,7 +170,9 @@ extern "C" int bs_index_attach_rabitq(bs_index ix, const uint32_t* codes, const 
             std::memcpy(rec, vtmp.data() + i * ix->dstride, 4ull * ix->dstride);
             std::memcpy(rec + ix->rec_ids, etmp.data() + i * R, 4ull * R);
             std::memcpy(rec + ix->rec_fac, factors + (r0 + i) * 3 * R, 12ull * R);
-            std::memcpy(rec + ix->rec_codes, codes + (r0 + i) * R * wpp, 4ull * R * wpp);
+            const uint32_t* src = codes + (r0 + i) * R * wpp;
+            for (uint32_t j = 0; j < R; ++j)
+                std::memcpy(rec + ix->rec_codes + j * cws, src + j * wpp, 4ull * wpp);
         }
         HIP_TRY(hipMemcpy(ix->d_recs + r0 * rw, host.data(), m * rw * 4ull, hipMemcpyHostToDevice));
     }
@@ -267,6 +270,7 @@ int make_plan(bs_index ix, const bs_search_cfg* cfg, uint64_t nq, Plan& pl) {
         p.rec_ids = ix->rec_ids;
         p.rec_fac = ix->rec_fac;
         p.rec_codes = ix->rec_codes;
+        p.Q = bsd::quad_shape(ix->wpp, ix->degree);
         scratch = std::max(scratch, 4u * ix->pdim + 24u * ix->wpp);
     }
     auto al = [](uint32_t v) { return (v + 15u) & ~15u; };
@@ -288,7 +292,9 @@ int make_plan(bs_index ix, const bs_search_cfg* cfg, uint64_t nq, Plan& pl) {
 hipError_t launch(const Plan& pl, hipStream_t s) {
     switch (pl.mode) {
     case BS_GROUP_BLOOM: return bsd::launch_search_bloom(pl.p, pl.TR, pl.CR, pl.QMAX, pl.grid, pl.block, pl.lds, s);
-    case BS_RABITQ: return bsd::launch_search_rabitq(pl.p, pl.TR, pl.CR, pl.QMAX, pl.grid, pl.block, pl.lds, s);
+    case BS_RABITQ:
+        if (pl.p.wpp <= 4) return bsd::launch_search_rabitq(pl.p, pl.TR, pl.CR, pl.QMAX, pl.grid, pl.block, pl.lds, s);
+        return bsd::launch_search_rabitq_wide(pl.p, pl.TR, pl.CR, pl.QMAX, pl.grid, pl.block, pl.lds, s);
     default: return bsd::launch_search_hash(pl.p, pl.TR, pl.CR, pl.QMAX, pl.grid, pl.block, pl.lds, s);
     }
 }

@@ -112,9 +112,21 @@ __global__ void __launch_bounds__(64) dbg_fastscan_kernel(const float* query, co
     const uint32_t lane = bsd::lane_id();
     const uint32_t wpp = pdim / 32u;
     const bsd::QuantOut qo = bsd::quantize(query, signs, dim, pdim, seed, scr, planes, codes_out);
-    uint32_t pl[6];
-    bsd::lane_planes(planes, wpp, pl);
-    bsd::raw_sums(pl, codes_nbr, nn, wpp, rawbuf);
+    // codes_nbr: nn neighbours of cws = max(wpp, 4) words each (the record layout)
+    const bsd::QuadShape S = bsd::quad_shape(wpp, nn);
+    uint32_t pl[6][4];
+    bsd::lane_plane_quads(planes, wpp, S, pl);
+    if (S.qpn == 1) {
+        const uint32_t r = bsd::raw_quad(pl, bsd::load_quad(codes_nbr, lane, nn, 0u, S));
+        if (lane < nn) rawbuf[lane] = r;
+        bsd::wave_sync();
+    } else {
+        const uint32_t qi = lane & (S.qpn - 1), nl = lane >> S.qshift;
+        uint4 c0[4];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) c0[t] = bsd::load_quad(codes_nbr, static_cast<uint32_t>(t) * S.npp + nl, nn, qi, S);
+        bsd::raw_sums_wide(pl, codes_nbr, nn, S, c0, rawbuf);
+    }
     if (lane < nn) {
         const uint32_t raw = rawbuf[lane];
         raw_out[lane] = raw;
@@ -146,14 +158,18 @@ extern "C" int bs_debug_fastscan(const float* query, const float* signs, uint32_
     DTRY(dfac.alloc(3 * degree));
     DTRY(dscal.alloc(2));
     DTRY(dest.alloc(nn));
-    DTRY(dcodes.alloc(static_cast<size_t>(nn) * wpp));
+    const uint32_t cws = bsd::quad_shape(wpp, nn).cws;
+    std::vector<uint32_t> padded(static_cast<size_t>(nn) * cws, 0u);
+    for (uint32_t j = 0; j < nn; ++j)
+        for (uint32_t w = 0; w < wpp; ++w) padded[static_cast<size_t>(j) * cws + w] = codes_nbr[static_cast<size_t>(j) * wpp + w];
+    DTRY(dcodes.alloc(padded.size()));
     DTRY(draw.alloc(nn));
     DTRY(dco.alloc(pdim));
     DTRY(dsum.alloc(1));
     DTRY(hipMemcpy(dq.p, query, dim * 4, hipMemcpyHostToDevice));
     DTRY(hipMemcpy(ds.p, signs, pdim * 4, hipMemcpyHostToDevice));
     DTRY(hipMemcpy(dfac.p, factors, 3 * degree * 4, hipMemcpyHostToDevice));
-    DTRY(hipMemcpy(dcodes.p, codes_nbr, static_cast<size_t>(nn) * wpp * 4, hipMemcpyHostToDevice));
+    DTRY(hipMemcpy(dcodes.p, padded.data(), padded.size() * 4, hipMemcpyHostToDevice));
     const size_t lds = 4u * pdim + 24u * wpp + 4u * 64u;
     hipLaunchKernelGGL(dbg_fastscan_kernel, dim3(1), dim3(64), lds, nullptr, dq.p, ds.p, dim, pdim, seed, dcodes.p,
                        dfac.p, nn, degree, exact, dco.p, dscal.p, dsum.p, draw.p, dest.p);

@@ -418,15 +418,14 @@ __host__ __device__ inline L2Shape l2_shape(uint32_t dim) {
     return L;
 }
 
-// Partial sums of PB rows (one row per lane group per pass).  Every load is issued
-// unconditionally -- chunks outside the row are redirected to chunk 0 of the same row and
-// their difference is zeroed -- so all PB*QMAX loads of a lane are in flight together
-// (a conditional load would be followed by its own wait before the next one issues).
-// rows[t] must point at a valid row for every lane (inactive lane groups pass row 0).
+// Loads of PB rows (one row per lane group per pass), issued without waiting.  Every
+// load is unconditional -- chunks outside the row are redirected to chunk 0 of the same
+// row (l2_accum zeroes their difference) -- so all PB*QMAX loads of a lane are in flight
+// together (a conditional load would be followed by its own wait before the next one
+// issues).  rows[t] must point at a valid row for every lane (inactive groups pass row 0).
 template <int QMAX, int PB>
-__device__ __forceinline__ void l2_partials(const float4 (&q)[QMAX], const float* const (&rows)[PB], uint32_t lig,
-                                            const L2Shape& L, float (&p)[PB]) {
-    float4 v[PB][QMAX];
+__device__ __forceinline__ void l2_load(const float* const (&rows)[PB], uint32_t lig, const L2Shape& L,
+                                        float4 (&v)[PB][QMAX]) {
 #pragma unroll
     for (int t = 0; t < PB; ++t) {
         const float4* r4 = reinterpret_cast<const float4*>(rows[t]);
@@ -437,6 +436,13 @@ __device__ __forceinline__ void l2_partials(const float4 (&q)[QMAX], const float
             v[t][kk] = r4[ok ? j : 0u];
         }
     }
+}
+
+// Lane partial sums of squared differences of the rows loaded by l2_load, in chunk order
+// with explicit fma (the order the oracle's wave L2 restates).
+template <int QMAX, int PB>
+__device__ __forceinline__ void l2_accum(const float4 (&q)[QMAX], const float4 (&v)[PB][QMAX], uint32_t lig,
+                                         const L2Shape& L, float (&p)[PB]) {
     const bool full = L.QR * L.G == L.chunks && L.QR == static_cast<uint32_t>(QMAX);
 #pragma unroll
     for (int t = 0; t < PB; ++t) {
@@ -455,6 +461,14 @@ __device__ __forceinline__ void l2_partials(const float4 (&q)[QMAX], const float
         }
         p[t] = acc;
     }
+}
+
+template <int QMAX, int PB>
+__device__ __forceinline__ void l2_partials(const float4 (&q)[QMAX], const float* const (&rows)[PB], uint32_t lig,
+                                            const L2Shape& L, float (&p)[PB]) {
+    float4 v[PB][QMAX];
+    l2_load<QMAX, PB>(rows, lig, L, v);
+    l2_accum<QMAX, PB>(q, v, lig, L, p);
 }
 
 // query chunks of this lane: chunk j = lig + k*G, components beyond dim are 0
@@ -610,52 +624,90 @@ __device__ __forceinline__ float estimate(uint32_t raw, int32_t sum_q, float wid
     return est;
 }
 
-// raw = sum_b 2^b * popcount(plane_b & code) over one code word (the lane's word)
-__device__ __forceinline__ uint32_t raw_word(const uint32_t (&pl)[6], uint32_t code) {
-    uint32_t r = 0;
-#pragma unroll
-    for (int b = 0; b < 6; ++b) r += static_cast<uint32_t>(__builtin_popcount(pl[b] & code)) << b;
-    return r;
+// ---------------------------------------------------------------------------
+// Fastscan sums in the quad layout.  In a node record the codes of one neighbour are
+// cws = max(wpp, 4) words (words >= wpp are zero), so a lane reads four code words of
+// one neighbour with one 16-byte load.  Lane l works on quad l % qpn (qpn = cws / 4) of
+// neighbour pass * npp + l / qpn (npp = 64 / qpn).  With wpp <= 4 ("narrow", pdim <= 128)
+// a lane holds a whole neighbour and every lane uses the same plane words; otherwise
+// ("wide") the qpn partial sums of a neighbour are combined by an xor butterfly (exact
+// integer adds).
+// ---------------------------------------------------------------------------
+struct QuadShape {
+    uint32_t cws, qpn, qshift, npp, passes;
+};
+
+__host__ __device__ inline QuadShape quad_shape(uint32_t wpp, uint32_t R) {
+    QuadShape S;
+    S.cws = wpp < 4 ? 4u : wpp;
+    S.qpn = S.cws / 4;
+    S.qshift = 0;
+    while ((1u << S.qshift) < S.qpn) ++S.qshift;
+    S.npp = 64u / S.qpn;
+    S.passes = (R + S.npp - 1) / S.npp;
+    return S;
 }
 
-// Integer fastscan sums of R neighbours (fastscan.cuh:346-355): raw[n] = sum over the
-// dims whose code bit is set of the query's 6-bit code.  Lane l works on neighbour
-// l / wpp, code word l % wpp (its plane words `pl` are those of word l % wpp); the wpp
-// word sums of a neighbour are combined by an xor butterfly (exact integer adds).
-// codes: R*wpp words (global), rawbuf: R words of LDS.
-__device__ __forceinline__ void raw_sums(const uint32_t (&pl)[6], const uint32_t* codes, uint32_t R,
-                                         uint32_t wpp, uint32_t* rawbuf) {
-    const uint32_t lane = lane_id();
-    const uint32_t npp = 64u / wpp;
-    const uint32_t npass = (R + npp - 1) / npp;
-    const uint32_t nl = lane / wpp, w = lane & (wpp - 1);
-    for (uint32_t t0 = 0; t0 < npass; t0 += 4) {
-        uint32_t acc[4], code[4];
+// the lane's plane words: pl[b][k] = word 4 * (lane % qpn) + k of plane b (0 beyond wpp),
+// from the planes quantize() left in LDS
+__device__ __forceinline__ void lane_plane_quads(const uint32_t* planes, uint32_t wpp, const QuadShape& S,
+                                                 uint32_t (&pl)[6][4]) {
+    const uint32_t qi = lane_id() & (S.qpn - 1);
 #pragma unroll
-        for (int t = 0; t < 4; ++t) {  // unconditional loads (index clamped) so all 4 are in flight
-            const uint32_t nb = (t0 + static_cast<uint32_t>(t)) * npp + nl;
-            code[t] = codes[(nb < R ? nb : 0u) * wpp + w];
-        }
+    for (int b = 0; b < 6; ++b) {
 #pragma unroll
-        for (int t = 0; t < 4; ++t) {
-            const uint32_t nb = (t0 + static_cast<uint32_t>(t)) * npp + nl;
-            acc[t] = raw_word(pl, nb < R ? code[t] : 0u);
-        }
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-            const uint32_t s = bsw::group_sum_u32(acc[t], wpp);
-            const uint32_t nb = (t0 + static_cast<uint32_t>(t)) * npp + nl;
-            if (w == 0 && nb < R) rawbuf[nb] = s;
+        for (int k = 0; k < 4; ++k) {
+            const uint32_t w = 4u * qi + static_cast<uint32_t>(k);
+            pl[b][k] = (w < wpp) ? planes[static_cast<uint32_t>(b) * wpp + w] : 0u;
         }
     }
     wave_sync();
 }
 
-// the lane's six plane words (word index lane % wpp) after quantize()
-__device__ __forceinline__ void lane_planes(const uint32_t* planes, uint32_t wpp, uint32_t (&pl)[6]) {
-    const uint32_t w = lane_id() & (wpp - 1);
+// the four code words of quad `qi` of neighbour nb (nb >= R reads neighbour 0: every
+// load is issued unconditionally; the caller ignores the result)
+__device__ __forceinline__ uint4 load_quad(const uint32_t* codes, uint32_t nb, uint32_t R, uint32_t qi,
+                                           const QuadShape& S) {
+    const uint32_t n = nb < R ? nb : 0u;
+    return *reinterpret_cast<const uint4*>(codes + static_cast<uint64_t>(n) * S.cws + 4u * qi);
+}
+
+// raw = sum_b 2^b * popcount(plane_b & code) over the four words of a quad
+__device__ __forceinline__ uint32_t raw_quad(const uint32_t (&pl)[6][4], uint4 c) {
+    uint32_t r = 0;
 #pragma unroll
-    for (int b = 0; b < 6; ++b) pl[b] = planes[b * wpp + w];
+    for (int b = 0; b < 6; ++b) {
+        uint32_t n = static_cast<uint32_t>(__builtin_popcount(pl[b][0] & c.x));
+        n += static_cast<uint32_t>(__builtin_popcount(pl[b][1] & c.y));
+        n += static_cast<uint32_t>(__builtin_popcount(pl[b][2] & c.z));
+        n += static_cast<uint32_t>(__builtin_popcount(pl[b][3] & c.w));
+        r += n << b;
+    }
+    return r;
+}
+
+// Wide layout: raw sums of neighbours [0, R) into rawbuf (LDS).  c0 holds the lane's
+// quads of passes 0..3, issued by the caller together with its other loads; later
+// passes are loaded here, four at a time.
+__device__ __forceinline__ void raw_sums_wide(const uint32_t (&pl)[6][4], const uint32_t* codes, uint32_t R,
+                                              const QuadShape& S, const uint4 (&c0)[4], uint32_t* rawbuf) {
+    const uint32_t lane = lane_id();
+    const uint32_t qi = lane & (S.qpn - 1), nl = lane >> S.qshift;
+    uint4 c[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) c[t] = c0[t];
+    for (uint32_t t0 = 0; t0 < S.passes; t0 += 4) {
+        if (t0 > 0) {
+#pragma unroll
+            for (int t = 0; t < 4; ++t) c[t] = load_quad(codes, (t0 + static_cast<uint32_t>(t)) * S.npp + nl, R, qi, S);
+        }
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            const uint32_t nb = (t0 + static_cast<uint32_t>(t)) * S.npp + nl;
+            const uint32_t s = bsw::group_sum_u32(raw_quad(pl, c[t]), S.qpn);
+            if (qi == 0 && nb < R) rawbuf[nb] = s;
+        }
+    }
     wave_sync();
 }
 

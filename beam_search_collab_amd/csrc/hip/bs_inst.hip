@@ -1,5 +1,6 @@
 // Explicit search-kernel instances for one mode (BS_INST_MODE = 0 hash, 1 bloom,
-// 2 rabitq), compiled once per mode so the instances build in parallel.
+// 2 rabitq, 3 rabitq with wide codes), compiled once per mode so the instances build in
+// parallel.
 #include "bs_launch.hpp"
 
 #ifndef BS_INST_MODE
@@ -51,9 +52,14 @@ hipError_t launch_search_bloom(const SearchParams& p, int TR, int CR, int QMAX, 
                                hipStream_t s) {
     return launch_any(p, TR, CR, QMAX, g, b, lds, s);
 }
-#else
+#elif BS_INST_MODE == 2
 hipError_t launch_search_rabitq(const SearchParams& p, int TR, int CR, int QMAX, dim3 g, dim3 b, size_t lds,
                                 hipStream_t s) {
+    return launch_any(p, TR, CR, QMAX, g, b, lds, s);
+}
+#else
+hipError_t launch_search_rabitq_wide(const SearchParams& p, int TR, int CR, int QMAX, dim3 g, dim3 b, size_t lds,
+                                     hipStream_t s) {
     return launch_any(p, TR, CR, QMAX, g, b, lds, s);
 }
 #endif

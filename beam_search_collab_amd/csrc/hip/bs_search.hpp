@@ -10,7 +10,9 @@
 
 namespace bsd {
 
-enum { MODE_HASH = 0, MODE_BLOOM = 1, MODE_RABITQ = 2 };
+// MODE_RABITQ: codes of at most 4 words per neighbour (pdim <= 128), one neighbour per
+// lane; MODE_RABITQ_WIDE: longer codes, a neighbour spread over pdim / 128 lanes.
+enum { MODE_HASH = 0, MODE_BLOOM = 1, MODE_RABITQ = 2, MODE_RABITQ_WIDE = 3 };
 
 struct SearchParams {
     const float* vecs;      // n * dstride (zero-padded rows)
@@ -27,6 +29,7 @@ struct SearchParams {
     uint32_t entry;
     int32_t max_it, reset;
     uint32_t pdim, wpp, rec_words, rec_ids, rec_fac, rec_codes;  // record offsets (words)
+    QuadShape Q;            // code layout of a record (quad_shape(wpp, R))
     uint32_t lds_wave;      // bytes of LDS per wavefront
     uint32_t off_filter, off_scratch, off_cand;  // byte offsets inside the wave slice
     L2Shape L;
@@ -58,7 +61,7 @@ __global__ void __launch_bounds__(512) search_kernel(const SearchParams p) {
 
     uint32_t n_iter = 0, n_exp = 0, n_dist = 0, n_est = 0, n_rr = 0;
 
-    if constexpr (MODE != MODE_RABITQ) {
+    if constexpr (MODE == MODE_HASH || MODE == MODE_BLOOM) {
         // ------------------------------------------------------------------ base
         HashLds hf;
         BloomLds bf;
@@ -197,14 +200,24 @@ __global__ void __launch_bounds__(512) search_kernel(const SearchParams p) {
         const uint64_t rstride = p.rec_words;
         const float* rbase = reinterpret_cast<const float*>(p.recs);
 
-        // quantize the query; the lane's plane words for word index (lane % wpp)
-        uint32_t pl[6];
+        constexpr bool WIDE = MODE == MODE_RABITQ_WIDE;
+        const QuadShape S = p.Q;
+        const uint32_t qi = lane & (S.qpn - 1), nl = lane >> S.qshift;
+
+        // quantize the query; the lane's plane words (wave-uniform in the narrow layout)
+        uint32_t pl[6][4];
         QuantOut qo;
         {
             float* qscr = reinterpret_cast<float*>(scratch);
             uint32_t* planes = reinterpret_cast<uint32_t*>(my + p.off_scratch + 4u * p.pdim);
             qo = quantize(qv, p.signs, p.dim, p.pdim, 0u, qscr, planes, nullptr);
-            lane_planes(planes, wpp, pl);
+            lane_plane_quads(planes, wpp, S, pl);
+            if constexpr (!WIDE) {
+#pragma unroll
+                for (int b = 0; b < 6; ++b)
+#pragma unroll
+                    for (int k = 0; k < 4; ++k) pl[b][k] = uniform(pl[b][k]);
+            }
         }
         hf.clear();
 
@@ -225,34 +238,63 @@ __global__ void __launch_bounds__(512) search_kernel(const SearchParams p) {
             if (!hf.insert1(parent)) continue;  // already expanded (gpu_search_rabitq.cuh:249-252)
             ++n_exp;
             const uint32_t* rec = p.recs + static_cast<uint64_t>(parent) * rstride;
-            // neighbour ids, filtered by the expanded set
+            const float* fac = reinterpret_cast<const float*>(rec + p.rec_fac);
+            const uint32_t* codes = rec + p.rec_codes;
+            // Every load of the record -- neighbour ids, factors, the parent's vector and
+            // (the first four passes of) the codes -- is issued before any result is used,
+            // so an expansion costs one HBM round trip.  Indices are clamped, not masked.
             uint32_t child[CR];
-            bool valid[CR];
+            float ftx[CR], ffd[CR], ffv[CR];
 #pragma unroll
             for (int rc = 0; rc < CR; ++rc) {
                 const uint32_t i = static_cast<uint32_t>(rc) * 64u + lane;
-                child[rc] = (i < p.R) ? rec[p.rec_ids + i] : INVALID;
+                const uint32_t ic = i < p.R ? i : 0u;
+                child[rc] = rec[p.rec_ids + ic];
+                ftx[rc] = fac[ic];
+                ffd[rc] = fac[p.R + ic];
+                ffv[rc] = fac[2 * p.R + ic];
             }
-            const float exact = l2_one<QMAX>(q, reinterpret_cast<const float*>(rec), L);
-            ++n_dist;
+            float4 pv[1][QMAX];
+            {
+                const float* const rows[1] = {reinterpret_cast<const float*>(rec)};
+                l2_load<QMAX, 1>(rows, lig, L, pv);
+            }
+            constexpr int NC = WIDE ? 4 : CR;
+            uint4 cw[NC];
 #pragma unroll
-            for (int rc = 0; rc < CR; ++rc) valid[rc] = child[rc] != INVALID && !hf.contains_lane(child[rc]);
-            raw_sums(pl, rec + p.rec_codes, p.R, wpp, rawbuf);
+            for (int t = 0; t < NC; ++t) {
+                const uint32_t nb = WIDE ? static_cast<uint32_t>(t) * S.npp + nl : static_cast<uint32_t>(t) * 64u + lane;
+                cw[t] = load_quad(codes, nb, p.R, qi, S);
+            }
+
+            // exact distance of the parent
+            float pe[1];
+            l2_accum<QMAX, 1>(q, pv, lig, L, pe);
+            const float exact = __uint_as_float(readlane(__float_as_uint(bsw::group_sum(pe[0], L.G)), 0));
+            ++n_dist;
+            // fastscan sums of the neighbours
+            uint32_t raw[CR];
+            if constexpr (WIDE) {
+                const uint4(&c0)[4] = reinterpret_cast<const uint4(&)[4]>(cw);
+                raw_sums_wide(pl, codes, p.R, S, c0, rawbuf);
+#pragma unroll
+                for (int rc = 0; rc < CR; ++rc) {
+                    const uint32_t i = static_cast<uint32_t>(rc) * 64u + lane;
+                    raw[rc] = rawbuf[i < p.R ? i : 0u];
+                }
+            } else {
+#pragma unroll
+                for (int rc = 0; rc < CR; ++rc) raw[rc] = raw_quad(pl, cw[rc < NC ? rc : 0]);
+            }
             uint64_t ck[CR], cm[CR];
             uint32_t nv = 0;
 #pragma unroll
             for (int rc = 0; rc < CR; ++rc) {
                 const uint32_t i = static_cast<uint32_t>(rc) * 64u + lane;
-                uint64_t k = EMPTY_KEY;
-                {
-                    const float* fac = reinterpret_cast<const float*>(rec + p.rec_fac);
-                    const uint32_t ic = i < p.R ? i : 0u;  // unconditional loads, index clamped
-                    const float tx = fac[ic], fdq = fac[p.R + ic], fvq = fac[2 * p.R + ic];
-                    const float est = estimate(rawbuf[ic], qo.sum_q, qo.width, qo.low, tx, fdq, fvq, exact);
-                    if (valid[rc]) k = make_key(est, child[rc]);
-                }
-                ck[rc] = k;
-                cm[rc] = ballot(valid[rc]);
+                const bool valid = i < p.R && child[rc] != INVALID && !hf.contains_lane(child[rc]);
+                const float est = estimate(raw[rc], qo.sum_q, qo.width, qo.low, ftx[rc], ffd[rc], ffv[rc], exact);
+                ck[rc] = valid ? make_key(est, child[rc]) : EMPTY_KEY;
+                cm[rc] = ballot(valid);
                 nv += static_cast<uint32_t>(__builtin_popcountll(cm[rc]));
             }
             wave_sync();

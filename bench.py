@@ -1,13 +1,18 @@
-"""Benchmark of the GPU graph beam search on one MI355X (BASELINE.json configs[1]).
+"""Benchmark of the GPU graph beam search on one MI355X.
 
-Workload (synthetic, seeded): 1M x 128 fp32 base from a 64-centre Gaussian mixture
-(centres ~U[0,128], sigma 12, clamped >= 0), 10k queries drawn the same way, degree-32
-Vamana graph (beam 128, alpha 2.0, seed 1234), base mode K=100, topk_size=256,
-filter_capacity=1024, reset_interval=16, max_iterations=1024.  A "step" is one search of
-all 10k queries with the queries already resident in HBM.
+Default workload = BASELINE config B: 1M x 128 fp32 base from a 64-centre Gaussian
+mixture (centres ~U[0,128], sigma 12, clamped >= 0), 10k queries drawn the same way,
+degree-32 Vamana graph (beam 128, alpha 2.0, seed 1234), base mode K=100,
+topk_size=256, filter_capacity=1024, reset_interval=16, max_iterations=1024.  A "step"
+is one search of all queries with the queries already resident in HBM.
 
-    python bench.py [--gpus 1] [--steps 5] [--warmup 1] [--n 1000000] [--nq 10000]
-                    [--mode base] [--topk 256] [--K 100] [--no-cpu]
+    python bench.py [--gpus 1] [--steps 5] [--warmup 1] [--config B] [--mode base]
+                    [--topk 256] [--K 100] [--sweep 64,128,512] [--sweep-modes warp2,bwarp2]
+                    [--no-cpu]
+
+--config selects the other synthetic workloads of the survey (A: 100k x 128 topk 64;
+C: B + rabitq codebook seed 12345, K=10; D: 1.2M x 100 N(0,1) L2-normalised, degree 64,
+topk 128, K=10, warp1; E: 1M x 960, 256 centres ~U[0,1], sigma 0.05, 1k queries).
 
 Prints one JSON line (see the repository contract) with `roofline` (algorithmic bytes of
 the search kernel / its average launch time, HIP events on the launch stream) and
@@ -27,6 +32,15 @@ sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
 
+# synthetic workloads (seeds: centres 101, base 202, queries 303)
+CONFIGS = {
+    "A": dict(n=100_000, nq=1_000, dim=128, degree=32, data="mix64", mode="base", K=10, topk=64),
+    "B": dict(n=1_000_000, nq=10_000, dim=128, degree=32, data="mix64", mode="base", K=100, topk=256),
+    "C": dict(n=1_000_000, nq=10_000, dim=128, degree=32, data="mix64", mode="rabitq", K=10, topk=256),
+    "D": dict(n=1_200_000, nq=10_000, dim=100, degree=64, data="normal", mode="warp1", K=10, topk=128),
+    "E": dict(n=1_000_000, nq=1_000, dim=960, degree=32, data="mix256", mode="base", K=100, topk=256),
+}
+
 
 def log(msg):
     print(f"[bench {time.strftime('%H:%M:%S')}] {msg}", file=sys.stderr, flush=True)
@@ -37,13 +51,12 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=5)
     ap.add_argument("--warmup", type=int, default=1)
-    ap.add_argument("--n", type=int, default=1_000_000)
-    ap.add_argument("--nq", type=int, default=10_000)
-    ap.add_argument("--dim", type=int, default=128)
-    ap.add_argument("--degree", type=int, default=32)
-    ap.add_argument("--mode", default="base")
-    ap.add_argument("--topk", type=int, default=256)
-    ap.add_argument("--K", type=int, default=100)
+    ap.add_argument("--config", default="B", choices=sorted(CONFIGS))
+    ap.add_argument("--n", type=int, default=None)
+    ap.add_argument("--nq", type=int, default=None)
+    ap.add_argument("--mode", default=None)
+    ap.add_argument("--topk", type=int, default=None)
+    ap.add_argument("--K", type=int, default=None)
     ap.add_argument("--cap", type=int, default=1024)
     ap.add_argument("--reset", type=int, default=16)
     ap.add_argument("--max-it", type=int, default=1024)
@@ -51,14 +64,36 @@ def parse():
     ap.add_argument("--cpu-procs", type=int, default=0)
     ap.add_argument("--cpu-queries", type=int, default=400, help="queries per CPU process")
     ap.add_argument("--sweep", default="", help="comma list of topk values to sweep (extra lines on stderr)")
+    ap.add_argument("--sweep-modes", default="", help="comma list of modes to time as well (lines on stderr)")
+    ap.add_argument("--cache", default="", help="directory to keep the generated data, graph and ground truth "
+                                                   "in between runs (npz, untimed)")
     ap.add_argument("--calib-copy-mib", type=int, default=0,
                     help="run one elementwise copy of this many MiB first (HBM-counter calibration under rocprofv3)")
-    return ap.parse_args()
+    a = ap.parse_args()
+    c = CONFIGS[a.config]
+    for k in ("n", "nq", "mode", "topk", "K"):
+        if getattr(a, k) is None:
+            setattr(a, k, c[k])
+    a.dim, a.degree, a.data = c["dim"], c["degree"], c["data"]
+    return a
+
+
+def gen_data(args):
+    from beam_search_collab_amd import host
+    if args.data == "mix64":
+        base = host.gen_mixture(args.n, args.dim, 64, 0.0, 128.0, 12.0, 0.0, 101, 202)
+        queries = host.gen_mixture(args.nq, args.dim, 64, 0.0, 128.0, 12.0, 0.0, 101, 303)
+    elif args.data == "mix256":
+        base = host.gen_mixture(args.n, args.dim, 256, 0.0, 1.0, 0.05, 0.0, 101, 202)
+        queries = host.gen_mixture(args.nq, args.dim, 256, 0.0, 1.0, 0.05, 0.0, 101, 303)
+    else:
+        base = host.gen_normalized(args.n, args.dim, 202)
+        queries = host.gen_normalized(args.nq, args.dim, 303)
+    return base, queries
 
 
 def gt_gpu(base_t, q_t, k, margin=28):
     """exact top-k: fp32 GEMM candidates on the GPU, exact fp64 re-scoring on the host"""
-    import numpy as np
     import torch
     from beam_search_collab_amd import host
     nq = q_t.shape[0]
@@ -85,88 +120,133 @@ def gt_gpu(base_t, q_t, k, margin=28):
     return host.groundtruth_refine(base_t.cpu().numpy(), q_t.cpu().numpy(), cand.cpu().numpy(), k)
 
 
-def cpu_baseline(files, nq_total, args, entry_line_check=None):
-    """reference cpu_cli on P query shards in parallel processes, one core each"""
-    import numpy as np
+def _run_cli_shards(ref, shards, files, args, mode, use_taskset):
+    """one reference cpu_cli process per shard (pinned to one core each); returns the
+    'time:' figure (ms) and the recall line of every shard"""
+    procs = []
+    for p, (qf, gf) in enumerate(shards):
+        data = {"graph": files["graph"], "base": files["base"], "query": qf, "gt": gf}
+        if mode == "rabitq":
+            data["codebook"] = files["codebook"]
+        cfg = {"data": data, "search": {"mode": mode, "K": args.K, "topk_size": args.topk,
+                                        "max_iterations": args.max_it}}
+        cmd = [ref]
+        if use_taskset:
+            cmd = ["taskset", "-c", str(p % (os.cpu_count() or 1))] + cmd
+        pr = subprocess.Popen(cmd, stdin=subprocess.PIPE, stdout=subprocess.PIPE, stderr=subprocess.PIPE, text=True)
+        pr.stdin.write(json.dumps(cfg))
+        pr.stdin.close()
+        procs.append(pr)
+    times, recalls = [], []
+    for pr in procs:
+        out = pr.stdout.read()
+        pr.wait()
+        if pr.returncode != 0:
+            raise RuntimeError("cpu_cli failed: " + pr.stderr.read()[-400:])
+        for line in out.splitlines():
+            if "time:" in line:
+                times.append(float(line.split("time:")[1].split("ms")[0]))
+            if line.startswith("recall@"):
+                recalls.append(float(line.split(":")[1]))
+    return times, recalls
+
+
+def cpu_baseline(files, nq_total, args):
+    """reference cpu_cli on P query shards in parallel processes, one core each.
+
+    The reference cpu_cli starts its clock before it parses a rabitq codebook
+    (src/cpu_cli.cpp:113-122), so for rabitq the same P processes also run once with a
+    single query each; the difference is the search-only time."""
     from beam_search_collab_amd import host
     from oracle import pyoracle as po
+    from shutil import which
     ref = os.path.join(po.REF_DIR, "cpu_cli")
+    cli_mode = "rabitq" if args.mode == "rabitq" else "base"
     P = args.cpu_procs or min(16, os.cpu_count() or 1)
     per = min(args.cpu_queries, nq_total // P)
     q = host.read_fvecs(files["query"])
     gt = host.read_ivecs(files["gt"])
-    shards = []
-    for p in range(P):
-        qs = q[p * per:(p + 1) * per]
-        qf = os.path.join(files["dir"], f"q_shard{p}.fvecs")
-        gf = os.path.join(files["dir"], f"gt_shard{p}.ivecs")
-        host.write_fvecs(qf, qs)
-        host.write_ivecs(gf, gt[p * per:(p + 1) * per])
-        shards.append((qf, gf))
+
+    def write_shards(count, tag):
+        shards = []
+        for p in range(P):
+            qf = os.path.join(files["dir"], f"q_{tag}{p}.fvecs")
+            gf = os.path.join(files["dir"], f"gt_{tag}{p}.ivecs")
+            host.write_fvecs(qf, q[p * per:p * per + count])
+            host.write_ivecs(gf, gt[p * per:p * per + count])
+            shards.append((qf, gf))
+        return shards
+
     if os.path.exists(ref):
-        procs = []
-        for p, (qf, gf) in enumerate(shards):
-            cfg = {"data": {"graph": files["graph"], "base": files["base"], "query": qf, "gt": gf},
-                   "search": {"mode": "base", "K": args.K, "topk_size": args.topk,
-                              "max_iterations": args.max_it}}
-            cmd = [ref]
-            if _has_taskset():
-                cmd = ["taskset", "-c", str(p % (os.cpu_count() or 1))] + cmd
-            pr = subprocess.Popen(cmd, stdin=subprocess.PIPE, stdout=subprocess.PIPE, stderr=subprocess.PIPE, text=True)
-            pr.stdin.write(json.dumps(cfg))
-            pr.stdin.close()
-            procs.append(pr)
-        times, recalls = [], []
-        for pr in procs:
-            out = pr.stdout.read()
-            pr.wait()
-            if pr.returncode != 0:
-                raise RuntimeError("cpu_cli failed: " + pr.stderr.read()[-400:])
-            for line in out.splitlines():
-                if "time:" in line:
-                    times.append(float(line.split("time:")[1].split("ms")[0]))
-                if line.startswith("recall@"):
-                    recalls.append(float(line.split(":")[1]))
-        qps_all = P * per / (max(times) / 1000.0)
-        qps_1 = per / (sum(times) / len(times) / 1000.0)
-        return {"value": round(qps_all, 1), "unit": "queries/s", "cores": P, "kind": "reference",
-                "sample": f"{P} processes x {per} queries of the same 10k-query workload (one core each, "
-                          f"taskset), reference cpu_cli base mode built from source, search time only",
-                "one_core_qps": round(qps_1, 1), "recall_at_K": round(sum(recalls) / len(recalls), 4)}
+        use_ts = which("taskset") is not None
+        times, recalls = _run_cli_shards(ref, write_shards(per, "s"), files, args, cli_mode, use_ts)
+        out = {"unit": "queries/s", "cores": P, "kind": "reference"}
+        if cli_mode == "rabitq":
+            t_load, _ = _run_cli_shards(ref, write_shards(1, "l"), files, args, cli_mode, use_ts)
+            search = [max(t - l, 1e-3) for t, l in zip(times, t_load)]
+            out["value"] = round(P * (per - 1) / (max(search) / 1000.0), 1)
+            out["one_core_qps"] = round((per - 1) / (sum(search) / len(search) / 1000.0), 1)
+            out["with_codebook_load_qps"] = round(P * per / (max(times) / 1000.0), 1)
+            out["sample"] = (f"{P} processes x {per} queries of the same workload (one core each, taskset), "
+                             f"reference cpu_cli rabitq built from source; search time = run time minus a "
+                             f"1-query run of the same processes (codebook parse)")
+        else:
+            out["value"] = round(P * per / (max(times) / 1000.0), 1)
+            out["one_core_qps"] = round(per / (sum(times) / len(times) / 1000.0), 1)
+            out["sample"] = (f"{P} processes x {per} queries of the same workload (one core each, taskset), "
+                             f"reference cpu_cli {cli_mode} mode built from source, search time only")
+        out["recall_at_K"] = round(sum(recalls) / len(recalls), 4)
+        return out
     # oracle port (single thread) when the reference binary is absent
     base = host.read_fvecs(files["base"])
     edges = host.read_graph(files["graph"])
-    oi = po.OracleIndex(base, edges)
+    if cli_mode == "rabitq":
+        oi = po.OracleIndex(base, edges, files["rq"][1], files["rq"][2], files["rq"][3])
+        om, entry = po.RABITQ_CPUREF, files["rq"][0]
+    else:
+        oi = po.OracleIndex(base, edges)
+        om, entry = po.BASE_CPUREF, files["entry"]
     t = time.time()
-    oi.search(q[:per], args.K, po.BASE_CPUREF, args.topk, files["entry"], args.max_it, args.cap, 0, po.L2_SEQ)
+    oi.search(q[:per], args.K, om, args.topk, entry, args.max_it, args.cap, 0, po.L2_SEQ)
     dt = time.time() - t
     return {"value": round(per / dt, 1), "unit": "queries/s", "cores": 1, "kind": "port",
-            "sample": f"{per} queries, CPU oracle restatement of cpu_search_base.hpp, one thread"}
+            "sample": f"{per} queries, CPU oracle restatement of the reference cpu_cli {cli_mode} search, one thread"}
 
 
-def kernel_name(args):
-    tr = 1 if args.topk <= 64 else 2 if args.topk <= 128 else 4 if args.topk <= 256 else 8
-    cr = 1 if args.degree <= 64 else 2
-    qm = 1 if (args.dim + 3) // 4 <= 64 else 4
-    mode = {"base": 0, "bwarp": 1, "rabitq": 2}.get(args.mode.rstrip("0123456789"), 0)
-    return f"bsd::search_kernel<{tr}, {cr}, {qm}, {mode}>"
+def kernel_name(mode, topk, degree):
+    """symbol of the search-kernel instance a launch uses (beam registers TR = topk/64,
+    candidate registers CR = degree/64, 4 float4 chunks per lane, filter/mode id)"""
+    tr = 1 if topk <= 64 else 2 if topk <= 128 else 4 if topk <= 256 else 8
+    cr = 1 if degree <= 64 else 2
+    m = {"base": 0, "warp": 0, "bwarp": 1, "rabitq": 2}[mode.rstrip("0123456789")]
+    return f"bsd::search_kernel<{tr}, {cr}, 4, {m}>"
 
 
 def measured_traffic(args):
     """HBM bytes per launch of the search kernel from the committed rocprofv3 --pmc summary
-    (FETCH_SIZE / WRITE_SIZE scaled by a 1 GiB copy), for the default workload only."""
-    default = (args.n, args.nq, args.dim, args.degree, args.mode, args.topk, args.K, args.cap, args.reset) == \
-        (1_000_000, 10_000, 128, 32, "base", 256, 100, 1024, 16)
-    path = os.path.join(ROOT, "profiles", "search_kernel_base_1Mx128_traffic.json")
+    (FETCH_SIZE / WRITE_SIZE scaled by a plain copy), for a config's default workload only."""
+    c = CONFIGS[args.config]
+    default = (args.n, args.nq, args.mode, args.topk, args.K, args.cap, args.reset, args.max_it) == \
+        (c["n"], c["nq"], c["mode"], c["topk"], c["K"], 1024, 16, 1024)
+    path = os.path.join(ROOT, "profiles", f"search_kernel_{args.mode}_config{args.config}_traffic.json")
     if not default or not os.path.exists(path):
         return None
     with open(path) as f:
         return json.load(f)["traffic_bytes"]
 
 
-def _has_taskset():
-    from shutil import which
-    return which("taskset") is not None
+def algorithmic_bytes(mode, nq, d, R, K, pq, pdim=0):
+    """bytes one launch must move at minimum, from the per-query counters
+    (iterations, expansions E, exact distances D, estimates, reranks T_r):
+      base/warp: nq*(4d + 4K) + E*4R + D*4d  (query, adjacency rows, gathered vectors, results)
+      rabitq:    nq*(4d + 4pdim + 4K) + E*(4R + 4R*wpp + 12R) + (D + T_r)*4d
+                 (query, sign table, per expansion ids + codes + 3 factors, parent and
+                 rerank vectors, results)"""
+    E, D, Tr = int(pq[:, 1].sum()), int(pq[:, 2].sum()), int(pq[:, 4].sum())
+    if mode == "rabitq":
+        wpp = pdim // 32
+        return nq * (4 * d + 4 * pdim + 4 * K) + E * (4 * R + 4 * R * wpp + 12 * R) + (D + Tr) * 4 * d
+    return nq * (4 * d + 4 * K) + E * 4 * R + D * 4 * d
 
 
 def main():
@@ -182,21 +262,37 @@ def main():
 
     assert torch.cuda.is_available(), "bench.py needs the GPU"
     dev = torch.device("cuda:0")
-    t0 = time.time()
-    base = host.gen_mixture(args.n, args.dim, 64, 0.0, 128.0, 12.0, 0.0, 101, 202)
-    queries = host.gen_mixture(args.nq, args.dim, 64, 0.0, 128.0, 12.0, 0.0, 101, 303)
-    log(f"data {args.n}x{args.dim}, {args.nq} queries: {time.time() - t0:.1f}s")
-    t1 = time.time()
-    edges = host.build_vamana(base, args.degree, 128, 2.0, 1234, exact=False, verbose=True)
-    log(f"Vamana graph R={args.degree}: {time.time() - t1:.1f}s")
-    t1 = time.time()
-    base_t = torch.from_numpy(base).to(dev)
-    q_t = torch.from_numpy(queries).to(dev)
-    gt = gt_gpu(base_t, q_t, 100)
-    del base_t
-    torch.cuda.empty_cache()
-    log(f"ground truth top-100: {time.time() - t1:.1f}s")
+    cache = os.path.join(args.cache, f"bench_{args.data}_{args.n}x{args.dim}_{args.nq}q_R{args.degree}.npz") if args.cache else ""
+    if cache and os.path.exists(cache):
+        z = np.load(cache)
+        base, queries, edges, gt = z["base"], z["queries"], z["edges"], z["gt"]
+        log(f"config {args.config}: data, graph and ground truth from {cache}")
+        q_t = torch.from_numpy(queries).to(dev)
+    else:
+        t0 = time.time()
+        base, queries = gen_data(args)
+        log(f"config {args.config}: data {args.n}x{args.dim} ({args.data}), {args.nq} queries: "
+            f"{time.time() - t0:.1f}s")
+        t1 = time.time()
+        edges = host.build_vamana(base, args.degree, 128, 2.0, 1234, exact=False, verbose=True)
+        log(f"Vamana graph R={args.degree}: {time.time() - t1:.1f}s")
+        t1 = time.time()
+        base_t = torch.from_numpy(base).to(dev)
+        q_t = torch.from_numpy(queries).to(dev)
+        gt = gt_gpu(base_t, q_t, 100)
+        del base_t
+        torch.cuda.empty_cache()
+        log(f"ground truth top-100: {time.time() - t1:.1f}s")
+        if cache:
+            os.makedirs(args.cache, exist_ok=True)
+            np.savez(cache, base=base, queries=queries, edges=edges, gt=gt)
     entry = host.entry_point(base)
+    need_rq = args.mode == "rabitq" or "rabitq" in args.sweep_modes
+    rq = None
+    if need_rq:
+        t1 = time.time()
+        rq = host.build_rabitq(base, edges, 12345)
+        log(f"rabitq codebook (seed 12345, pdim {rq[3].shape[0]}): {time.time() - t1:.1f}s")
     if args.calib_copy_mib:
         # a plain read-once/write-once kernel of known size: rocprofv3 --pmc FETCH_SIZE /
         # WRITE_SIZE on it gives the counter-to-bytes factor used for the search kernel
@@ -207,66 +303,86 @@ def main():
         log(f"calibration copy: {args.calib_copy_mib} MiB read + {args.calib_copy_mib} MiB written")
         del x, y
     g = search.GPUGraph(base, edges)
-    cfg = search.GPUBaseSearchCfg(args.topk, args.cap, entry, args.max_it, args.reset)
-    nq, K = args.nq, args.K
-    res_t = torch.empty((nq, K), dtype=torch.int32, device=dev)
-    pq_t = torch.zeros((nq, 5), dtype=torch.int32, device=dev)
+    if rq is not None:
+        g.attach_rabitq(rq[1], rq[2], rq[3])
+    pdim = rq[3].shape[0] if rq is not None else 0
+
+    def cfg_for(mode, topk):
+        if mode == "rabitq":
+            return search.GPURabitqSearchCfg(topk, args.cap, rq[0], args.max_it)
+        return search.GPUBaseSearchCfg(topk, args.cap, entry, args.max_it, args.reset)
+
+    nq, K, d, R = args.nq, args.K, args.dim, args.degree
     stream = torch.cuda.current_stream().cuda_stream
 
-    def step(per_query=0):
-        g.search_device(q_t.data_ptr(), nq, res_t.data_ptr(), K, args.mode, cfg, d_per_query=per_query,
-                        stream=stream)
+    def measure(mode, topk, k, steps, warmup):
+        """warm-up launches, then `steps` timed launches (HIP events on the launch stream);
+        returns (wall ms/step, avg kernel ms, ids, per-query counters)"""
+        cfg = cfg_for(mode, topk)
+        res_t = torch.empty((nq, k), dtype=torch.int32, device=dev)
+        pq_t = torch.zeros((nq, 5), dtype=torch.int32, device=dev)
 
-    for _ in range(args.warmup):
-        step(pq_t.data_ptr())
-    torch.cuda.synchronize()
-    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
-    torch.cuda.synchronize()
-    tt = time.time()
-    for s in range(args.steps):
-        ev[s][0].record()
-        step()
-        ev[s][1].record()
-    torch.cuda.synchronize()
-    wall = time.time() - tt
-    kms = [a.elapsed_time(b) for a, b in ev]
-    ms_per_step = wall * 1000.0 / args.steps
-    avg_kernel_ms = sum(kms) / len(kms)
-    ids = res_t.cpu().numpy().view(np.uint32)
+        def step(per_query=0):
+            g.search_device(q_t.data_ptr(), nq, res_t.data_ptr(), k, mode, cfg, d_per_query=per_query,
+                            stream=stream)
+
+        for _ in range(max(warmup, 1)):
+            step(pq_t.data_ptr())
+        torch.cuda.synchronize()
+        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+        torch.cuda.synchronize()
+        tt = time.time()
+        for s in range(steps):
+            ev[s][0].record()
+            step()
+            ev[s][1].record()
+        torch.cuda.synchronize()
+        wall = time.time() - tt
+        kms = [a.elapsed_time(b) for a, b in ev]
+        return wall * 1000.0 / steps, sum(kms) / len(kms), res_t.cpu().numpy().view(np.uint32), \
+            pq_t.cpu().numpy().astype(np.int64)
+
+    ms_per_step, avg_kernel_ms, ids, pq = measure(args.mode, args.topk, K, args.steps, args.warmup)
+    # r_k: the reference's definition (gpu_cli.cu:28-51) against the 100-column ground
+    # truth: the share of the K returned ids that are among the true 100 nearest;
+    # r_10: true 10-NN recall (first 10 returned ids against the true 10 nearest)
     r_k, dups = host.recall(ids, gt)
     r_10, _ = host.recall(ids[:, :10], gt[:, :10])
-    pq = pq_t.cpu().numpy().astype(np.int64)
     E, D = int(pq[:, 1].sum()), int(pq[:, 2].sum())
-    d, R = args.dim, args.degree
-    # base/warp byte model: B_q = 4d + E*4R + D*4d + 4K (query, adjacency rows, gathered
-    # vectors, results), summed over the launch's queries
-    bytes_launch = nq * (4 * d + 4 * K) + E * 4 * R + D * 4 * d
+    bytes_launch = algorithmic_bytes(args.mode, nq, d, R, K, pq, pdim)
     achieved = bytes_launch / (avg_kernel_ms / 1000.0) / 1e9
     qps = nq / (ms_per_step / 1000.0)
-    log(f"search: {ms_per_step:.2f} ms/step, kernel {avg_kernel_ms:.2f} ms, {qps:.0f} QPS, "
-        f"recall@{K} {r_k:.4f} recall@10 {r_10:.4f}, E/q {E / nq:.1f} D/q {D / nq:.1f}, "
+    log(f"search {args.mode}: {ms_per_step:.2f} ms/step, kernel {avg_kernel_ms:.2f} ms, {qps:.0f} QPS, "
+        f"recall@{K} (gpu_cli def.) {r_k:.4f} true recall@10 {r_10:.4f}, E/q {E / nq:.1f} D/q {D / nq:.1f}, "
         f"{achieved:.0f} GB/s algorithmic")
 
+    def side_line(mode, topk):
+        k2 = min(K, topk)
+        _, kms, i2, pq2 = measure(mode, topk, k2, 3, 1)
+        b2 = algorithmic_bytes(mode, nq, d, R, k2, pq2, pdim)
+        log(f"{mode} topk={topk} K={k2}: kernel {kms:.3f} ms, {nq / kms * 1000:.0f} QPS, "
+            f"true recall@10 {host.recall(i2[:, :10], gt[:, :10])[0]:.4f}, recall@{k2} (gpu_cli def.) "
+            f"{host.recall(i2, gt)[0]:.4f}, "
+            f"E/q {pq2[:, 1].sum() / nq:.1f} D/q {pq2[:, 2].sum() / nq:.1f}, {b2 / kms / 1e6:.0f} GB/s algorithmic")
+
     for tk in [int(x) for x in args.sweep.split(",") if x]:
-        c2 = search.GPUBaseSearchCfg(tk, args.cap, entry, args.max_it, args.reset)
-        k2 = min(K, tk)
-        r2 = torch.empty((nq, k2), dtype=torch.int32, device=dev)
-        st = g.search_device(q_t.data_ptr(), nq, r2.data_ptr(), k2, args.mode, c2, stream=stream, sync=True)
-        st = g.search_device(q_t.data_ptr(), nq, r2.data_ptr(), k2, args.mode, c2, stream=stream, sync=True)
-        i2 = r2.cpu().numpy().view(np.uint32)
-        log(f"sweep topk={tk}: kernel {st['kernel_ms']:.2f} ms, {nq / st['kernel_ms'] * 1000:.0f} QPS, "
-            f"recall@10 {host.recall(i2[:, :10], gt[:, :10])[0]:.4f}")
+        side_line(args.mode, tk)
+    for m in [x for x in args.sweep_modes.split(",") if x]:
+        side_line(m, args.topk)
 
     cpu = None
     if not args.no_cpu:
         t1 = time.time()
         tmp = tempfile.mkdtemp(prefix="bs_bench_")
         files = {"dir": tmp, "base": f"{tmp}/base.fvecs", "graph": f"{tmp}/graph.bin", "query": f"{tmp}/q.fvecs",
-                 "gt": f"{tmp}/gt.ivecs", "entry": entry}
+                 "gt": f"{tmp}/gt.ivecs", "entry": entry, "rq": rq}
         host.write_fvecs(files["base"], base)
         host.write_graph(files["graph"], edges)
         host.write_fvecs(files["query"], queries)
         host.write_ivecs(files["gt"], gt)
+        if args.mode == "rabitq":
+            files["codebook"] = f"{tmp}/codebook.bin"
+            host.write_codebook(files["codebook"], base, edges, rq[0], rq[1], rq[2], rq[3])
         cpu = cpu_baseline(files, nq, args)
         for f in os.listdir(tmp):
             os.remove(os.path.join(tmp, f))
@@ -285,17 +401,18 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f32",
-        "data": "synthetic (seeded 64-centre Gaussian mixture, built in-run)",
-        "config": {"workload": f"base-mode graph beam search, {args.n}x{args.dim} fp32, {nq} queries, "
-                               f"degree-{R} Vamana (beam 128, alpha 2.0, seed 1234)",
+        "dtype": "f32" if args.mode != "rabitq" else "u32 popcount + f32",
+        "data": f"synthetic (seeded, {args.data}, built in-run)",
+        "config": {"workload": f"config {args.config}: {args.mode} graph beam search, {args.n}x{args.dim} fp32, "
+                               f"{nq} queries, degree-{R} Vamana (beam 128, alpha 2.0, seed 1234)"
+                               + (", rabitq codebook seed 12345" if args.mode == "rabitq" else ""),
                    "mode": args.mode, "K": K, "topk_size": args.topk, "filter_capacity": args.cap,
                    "reset_interval": args.reset, "max_iterations": args.max_it,
-                   "recall_at_10": round(r_10, 4), f"recall_at_{K}": round(r_k, 4), "duplicates": dups,
+                   "recall_at_10": round(r_10, 4), f"recall_at_{K}_gpu_cli_def": round(r_k, 4), "duplicates": dups,
                    "expansions_per_query": round(E / nq, 2), "dist_evals_per_query": round(D / nq, 2)},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
-                     "kernel": kernel_name(args), "avg_launch_ms": round(avg_kernel_ms, 3),
+                     "kernel": kernel_name(args.mode, args.topk, R), "avg_launch_ms": round(avg_kernel_ms, 3),
                      "bytes_per_launch": bytes_launch},
         "cpu_baseline": cpu,
     }
