@@ -271,13 +271,18 @@ int make_plan(bs_index ix, const bs_search_cfg* cfg, uint64_t nq, Plan& pl) {
         p.rec_fac = ix->rec_fac;
         p.rec_codes = ix->rec_codes;
         p.Q = bsd::quad_shape(ix->wpp, ix->degree);
-        scratch = std::max(scratch, 4u * ix->pdim + 24u * ix->wpp);
+        // quantizer workspace (4 pdim B) and merge scratch overlap; the bit planes
+        // (6 planes of max(wpp, 4) words) follow both and live for the whole query
+        const uint32_t planes_at = std::max(scratch, 4u * ix->pdim);
+        scratch = planes_at + 24u * std::max(ix->wpp, 4u);
+        p.off_planes = planes_at;  // relative to off_scratch until the layout is fixed below
     }
     auto al = [](uint32_t v) { return (v + 15u) & ~15u; };
     p.off_filter = 0;
     p.off_scratch = al(filter_bytes);
     p.off_cand = p.off_scratch + al(scratch);
-    p.lds_wave = al(p.off_cand + 64u * pl.CR * 8u);
+    if (mode == BS_RABITQ) p.off_planes += p.off_scratch;
+    p.lds_wave = al(p.off_cand + 64u * pl.CR * 8u + 64u);  // + the merge's slot bitmap
     pl.lds = static_cast<size_t>(p.lds_wave) * ny;
     if (pl.lds > ix->max_lds)
         return fail(BS_EINVAL, "LDS per workgroup " + std::to_string(pl.lds) + " B exceeds the device limit " +

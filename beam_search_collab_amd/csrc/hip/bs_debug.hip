@@ -114,13 +114,18 @@ __global__ void __launch_bounds__(64) dbg_fastscan_kernel(const float* query, co
     const bsd::QuantOut qo = bsd::quantize(query, signs, dim, pdim, seed, scr, planes, codes_out);
     // codes_nbr: nn neighbours of cws = max(wpp, 4) words each (the record layout)
     const bsd::QuadShape S = bsd::quad_shape(wpp, nn);
-    uint32_t pl[6][4];
-    bsd::lane_plane_quads(planes, wpp, S, pl);
+    uint4 pl[6];
     if (S.qpn == 1) {
+        // narrow: the shared plane words go through LDS as in the search kernel
+        uint32_t* planes4 = reinterpret_cast<uint32_t*>(smem + ((4u * pdim + 24u * wpp + 256u + 15u) & ~15u));
+        bsd::store_planes4(planes, wpp, planes4);
+#pragma unroll
+        for (int b = 0; b < 6; ++b) pl[b] = reinterpret_cast<const uint4*>(planes4)[b];
         const uint32_t r = bsd::raw_quad(pl, bsd::load_quad(codes_nbr, lane, nn, 0u, S));
         if (lane < nn) rawbuf[lane] = r;
         bsd::wave_sync();
     } else {
+        bsd::lane_plane_quads(planes, wpp, S, pl);
         const uint32_t qi = lane & (S.qpn - 1), nl = lane >> S.qshift;
         uint4 c0[4];
 #pragma unroll
@@ -170,7 +175,7 @@ extern "C" int bs_debug_fastscan(const float* query, const float* signs, uint32_
     DTRY(hipMemcpy(ds.p, signs, pdim * 4, hipMemcpyHostToDevice));
     DTRY(hipMemcpy(dfac.p, factors, 3 * degree * 4, hipMemcpyHostToDevice));
     DTRY(hipMemcpy(dcodes.p, padded.data(), padded.size() * 4, hipMemcpyHostToDevice));
-    const size_t lds = 4u * pdim + 24u * wpp + 4u * 64u;
+    const size_t lds = ((4u * pdim + 24u * wpp + 4u * 64u + 15u) & ~15u) + 96u;
     hipLaunchKernelGGL(dbg_fastscan_kernel, dim3(1), dim3(64), lds, nullptr, dq.p, ds.p, dim, pdim, seed, dcodes.p,
                        dfac.p, nn, degree, exact, dco.p, dscal.p, dsum.p, draw.p, dest.p);
     DTRY(hipGetLastError());
@@ -203,7 +208,7 @@ __global__ void __launch_bounds__(64) dbg_beam_kernel(uint32_t T, const uint64_t
             ck[rc] = (j < bsize) ? keys[static_cast<uint64_t>(b) * bsize + j] : bsd::EMPTY_KEY;
             cm[rc] = bsd::ballot(ck[rc] != bsd::EMPTY_KEY);
         }
-        bsd::beam_merge<TR, CR>(beam, ck, cm, T, scratch);
+        bsd::beam_merge<TR, CR>(beam, ck, cm, T, scratch, scratch + 64 * TR);
         for (uint32_t k = 0; k < picks; ++k) {
             const uint32_t id = bsd::beam_pick<TR, RUN>(beam);
             if (lane == 0) picked[static_cast<uint64_t>(b) * picks + k] = id;
@@ -219,7 +224,7 @@ __global__ void __launch_bounds__(64) dbg_beam_kernel(uint32_t T, const uint64_t
 template <int TR, int CR>
 static void launch_beam(int run, uint32_t T, const uint64_t* k, uint32_t nb, uint32_t bs, uint32_t picks,
                         uint32_t* pk, uint64_t* bo) {
-    const size_t lds = 512u * TR;
+    const size_t lds = 512u * TR + 8u * (64u + 8u);  // merge scratch + aux
     if (run)
         hipLaunchKernelGGL((dbg_beam_kernel<TR, CR, true>), dim3(1), dim3(64), lds, nullptr, T, k, nb, bs, picks, pk, bo);
     else

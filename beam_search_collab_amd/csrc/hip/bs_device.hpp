@@ -48,34 +48,112 @@ __device__ __forceinline__ uint32_t key_id(uint64_t k) { return static_cast<uint
 // beam merge: keep the T smallest of (beam U candidates).
 // Replaces SharedBitonicTopK::merge / RegBitonicTopK::merge (topk_shared.cuh:272-331).
 // Candidates live in registers ck[CR] (candidate index j = rc*64 + lane), `cmask[rc]`
-// says which lanes hold one.  Ranks are computed by broadcasting each candidate once:
+// says which lanes hold one.  Final positions:
 //   beam element e moves to e + #(candidates < beam[e]);
 //   candidate j moves to #(beam <= cand_j) + #(candidates before j in (key, index)).
-// These positions are a permutation of 0..T+c-1; the first T are scattered to LDS and
-// read back in register-major order.  The cost is ~(3*TR+6) instructions per candidate,
-// which suits the few new candidates a base-mode expansion produces.
+// These positions are a permutation of 0..T+c-1; the first T form the new beam.
+// A candidate whose key is >= the beam's last key (EMPTY while the beam is not full)
+// lands at position >= T and is evicted (ties go after beam entries), so it is dropped
+// first.  Two ways to the same result:
+//  - rank loop: each remaining candidate is broadcast once and compared with every beam
+//    register, ~(3*TR+6) instructions per candidate (few candidates);
+//  - sorted merge (CR = 1, SORTED, at least BS_MERGE_SORT_MIN candidates): the candidates are
+//    compacted and bitonic-sorted across lanes, each finds its rank in the beam by a
+//    binary search of an LDS copy, the occupied output slots are marked in a bitmap and
+//    every output slot gathers its key from the candidate or the beam copy.
+// Identical keys are indistinguishable, so the two orders of equal candidates agree.
+// The sorted merge pays off where expansions add many candidates and registers are not
+// the occupancy limit (the RaBitQ loop); the base loop keeps the rank loop only.
+// LDS: scratch = 64*TR keys, aux = 64 + TR keys.
 // ---------------------------------------------------------------------------
-template <int TR, int CR>
+#ifndef BS_MERGE_SORT_MIN
+#define BS_MERGE_SORT_MIN 8
+#endif
+
+// ascending bitonic sort of the first P = pow2ceil(n) lanes (lanes beyond hold EMPTY)
+__device__ __forceinline__ uint64_t sort_lanes(uint64_t v, uint32_t n) {
+    const uint32_t lane = lane_id();
+#pragma unroll
+    for (uint32_t k = 2; k <= 64; k <<= 1) {
+        if (k / 2 >= n) break;
+#pragma unroll
+        for (uint32_t s = k >> 1; s >= 1; s >>= 1) {
+            const uint64_t p = bsw::xor_lane64_rt(v, s);
+            const bool keep_min = ((lane & s) == 0) == ((lane & k) == 0);
+            const bool lt = p < v;
+            v = (keep_min == lt) ? p : v;
+        }
+    }
+    return v;
+}
+
+template <int TR>
+__device__ __forceinline__ void beam_merge_sorted(uint64_t (&beam)[TR], uint64_t ck, uint64_t cmask, uint32_t n,
+                                                  uint32_t T, uint64_t* B, uint64_t* aux) {
+    const uint32_t lane = lane_id();
+    uint64_t* C = aux;       // 64 sorted candidates
+    uint64_t* M = aux + 64;  // TR words: bit s = output slot s holds a candidate
+    // compact the candidates to C[0..n), copy the beam to B, clear the bitmap
+    if ((cmask >> lane) & 1ull) C[bsw::lanes_below(cmask)] = ck;
+#pragma unroll
+    for (int r = 0; r < TR; ++r) B[static_cast<uint32_t>(r) * 64u + lane] = beam[r];
+    if (lane < static_cast<uint32_t>(TR)) M[lane] = 0ull;
+    wave_sync();
+    uint64_t c = lane < n ? C[lane] : EMPTY_KEY;
+    c = sort_lanes(c, n);
+    // rank in the beam: #(beam <= c).  Registers hold sorted runs of 64, so the run is
+    // chosen from the registers' last keys, then 6 halving steps inside it.
+    uint32_t lo = 0;
+#pragma unroll
+    for (int r = 0; r < TR - 1; ++r) lo += (readlane64(beam[r], 63) <= c) ? 64u : 0u;
+#pragma unroll
+    for (uint32_t step = 32; step >= 1; step >>= 1)
+        if (B[lo + step - 1] <= c) lo += step;
+    const uint32_t pos = lane + lo;
+    if (lane < n) {
+        C[lane] = c;
+        if (pos < T) __hip_atomic_fetch_or(&M[pos >> 6], 1ull << (pos & 63u), __ATOMIC_RELAXED,
+                                           __HIP_MEMORY_SCOPE_WAVEFRONT);
+    }
+    wave_sync();
+    uint32_t before = 0;  // candidates in the slots of earlier registers
+#pragma unroll
+    for (int r = 0; r < TR; ++r) {
+        const uint64_t mw = bsw::uniform64(M[r]);
+        const uint32_t s = static_cast<uint32_t>(r) * 64u + lane;
+        const uint32_t ob = before + bsw::lanes_below(mw);
+        const bool occ = (mw >> lane) & 1ull;
+        const uint64_t v = occ ? C[ob] : B[s - ob];
+        beam[r] = (s < T) ? v : EMPTY_KEY;
+        before += static_cast<uint32_t>(__builtin_popcountll(mw));
+    }
+    wave_sync();
+}
+
+template <int TR, int CR, bool SORTED = true>
 __device__ __forceinline__ void beam_merge(uint64_t (&beam)[TR], const uint64_t (&ck)[CR],
                                            const uint64_t (&cmask_in)[CR], uint32_t T,
-                                           uint64_t* lds_scratch) {
+                                           uint64_t* lds_scratch, uint64_t* lds_aux) {
     const uint32_t lane = lane_id();
-    // A candidate whose key is >= the beam's last key (EMPTY while the beam is not full)
-    // lands at position >= T and is evicted (ties go after beam entries), so it is dropped
-    // before the rank loop; the merged beam is the same.
     uint64_t thr = EMPTY_KEY;
     const uint32_t lr = (T - 1) >> 6, ll = (T - 1) & 63u;
 #pragma unroll
     for (int r = 0; r < TR; ++r)
         if (static_cast<uint32_t>(r) == lr) thr = readlane64(beam[r], ll);
     uint64_t cmask[CR];
-    bool any = false;
+    uint32_t n = 0;
 #pragma unroll
     for (int rc = 0; rc < CR; ++rc) {
         cmask[rc] = cmask_in[rc] & ballot(ck[rc] < thr);
-        any = any || cmask[rc] != 0;
+        n += static_cast<uint32_t>(__builtin_popcountll(cmask[rc]));
     }
-    if (!any) return;
+    if (n == 0) return;
+    if constexpr (CR == 1 && SORTED) {
+        if (n >= BS_MERGE_SORT_MIN) {
+            beam_merge_sorted<TR>(beam, ck[0], cmask[0], n, T, lds_scratch, lds_aux);
+            return;
+        }
+    }
     uint32_t bpos[TR];
 #pragma unroll
     for (int r = 0; r < TR; ++r) bpos[r] = static_cast<uint32_t>(r) * 64u + lane;
@@ -648,18 +726,31 @@ __host__ __device__ inline QuadShape quad_shape(uint32_t wpp, uint32_t R) {
     return S;
 }
 
-// the lane's plane words: pl[b][k] = word 4 * (lane % qpn) + k of plane b (0 beyond wpp),
+// the lane's plane words: pl[b] = words 4 * (lane % qpn) .. +3 of plane b (0 beyond wpp),
 // from the planes quantize() left in LDS
 __device__ __forceinline__ void lane_plane_quads(const uint32_t* planes, uint32_t wpp, const QuadShape& S,
-                                                 uint32_t (&pl)[6][4]) {
+                                                 uint4 (&pl)[6]) {
     const uint32_t qi = lane_id() & (S.qpn - 1);
 #pragma unroll
     for (int b = 0; b < 6; ++b) {
+        uint32_t w4[4];
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
             const uint32_t w = 4u * qi + static_cast<uint32_t>(k);
-            pl[b][k] = (w < wpp) ? planes[static_cast<uint32_t>(b) * wpp + w] : 0u;
+            w4[k] = (w < wpp) ? planes[static_cast<uint32_t>(b) * wpp + w] : 0u;
         }
+        pl[b] = make_uint4(w4[0], w4[1], w4[2], w4[3]);
+    }
+    wave_sync();
+}
+
+// Narrow layout: the 6 x 4 plane words every lane uses, padded to 4 words per plane
+// (planes4[4b + k]), kept in LDS for the whole query and re-read per expansion.
+__device__ __forceinline__ void store_planes4(const uint32_t* planes, uint32_t wpp, uint32_t* planes4) {
+    const uint32_t lane = lane_id();
+    if (lane < 24u) {
+        const uint32_t b = lane >> 2, k = lane & 3u;
+        planes4[lane] = (k < wpp) ? planes[b * wpp + k] : 0u;
     }
     wave_sync();
 }
@@ -673,14 +764,14 @@ __device__ __forceinline__ uint4 load_quad(const uint32_t* codes, uint32_t nb, u
 }
 
 // raw = sum_b 2^b * popcount(plane_b & code) over the four words of a quad
-__device__ __forceinline__ uint32_t raw_quad(const uint32_t (&pl)[6][4], uint4 c) {
+__device__ __forceinline__ uint32_t raw_quad(const uint4 (&pl)[6], uint4 c) {
     uint32_t r = 0;
 #pragma unroll
     for (int b = 0; b < 6; ++b) {
-        uint32_t n = static_cast<uint32_t>(__builtin_popcount(pl[b][0] & c.x));
-        n += static_cast<uint32_t>(__builtin_popcount(pl[b][1] & c.y));
-        n += static_cast<uint32_t>(__builtin_popcount(pl[b][2] & c.z));
-        n += static_cast<uint32_t>(__builtin_popcount(pl[b][3] & c.w));
+        uint32_t n = static_cast<uint32_t>(__builtin_popcount(pl[b].x & c.x));
+        n += static_cast<uint32_t>(__builtin_popcount(pl[b].y & c.y));
+        n += static_cast<uint32_t>(__builtin_popcount(pl[b].z & c.z));
+        n += static_cast<uint32_t>(__builtin_popcount(pl[b].w & c.w));
         r += n << b;
     }
     return r;
@@ -689,7 +780,7 @@ __device__ __forceinline__ uint32_t raw_quad(const uint32_t (&pl)[6][4], uint4 c
 // Wide layout: raw sums of neighbours [0, R) into rawbuf (LDS).  c0 holds the lane's
 // quads of passes 0..3, issued by the caller together with its other loads; later
 // passes are loaded here, four at a time.
-__device__ __forceinline__ void raw_sums_wide(const uint32_t (&pl)[6][4], const uint32_t* codes, uint32_t R,
+__device__ __forceinline__ void raw_sums_wide(const uint4 (&pl)[6], const uint32_t* codes, uint32_t R,
                                               const QuadShape& S, const uint4 (&c0)[4], uint32_t* rawbuf) {
     const uint32_t lane = lane_id();
     const uint32_t qi = lane & (S.qpn - 1), nl = lane >> S.qshift;

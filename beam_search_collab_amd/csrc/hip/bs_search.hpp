@@ -32,6 +32,7 @@ struct SearchParams {
     QuadShape Q;            // code layout of a record (quad_shape(wpp, R))
     uint32_t lds_wave;      // bytes of LDS per wavefront
     uint32_t off_filter, off_scratch, off_cand;  // byte offsets inside the wave slice
+    uint32_t off_planes;    // rabitq: the query's bit planes (outside the merge scratch)
     L2Shape L;
 };
 
@@ -47,6 +48,9 @@ __global__ void __launch_bounds__(512) search_kernel(const SearchParams p) {
     uint64_t* scratch = reinterpret_cast<uint64_t*>(my + p.off_scratch);
     uint32_t* cand_ids = reinterpret_cast<uint32_t*>(my + p.off_cand);
     float* cand_d = reinterpret_cast<float*>(my + p.off_cand) + 64 * CR;
+    // the merge's sorted candidates and slot bitmap reuse the candidate staging area
+    // (free once the keys are in registers), which has room for 64*CR + 8 keys
+    uint64_t* merge_aux = reinterpret_cast<uint64_t*>(my + p.off_cand);
 
     const L2Shape L = p.L;
     const uint32_t lig = lane & (L.G - 1);
@@ -109,7 +113,7 @@ __global__ void __launch_bounds__(512) search_kernel(const SearchParams p) {
             bool any = false;
 #pragma unroll
             for (int rc = 0; rc < CR; ++rc) any = any || (cm[rc] != 0);
-            if (any) beam_merge<TR, CR>(beam, ck, cm, T, scratch);
+            if (any) beam_merge<TR, CR, false>(beam, ck, cm, T, scratch, merge_aux);
 #pragma unroll
             for (int rc = 0; rc < CR; ++rc) cm[rc] = 0;
 
@@ -176,7 +180,7 @@ __global__ void __launch_bounds__(512) search_kernel(const SearchParams p) {
             bool any = false;
 #pragma unroll
             for (int rc = 0; rc < CR; ++rc) any = any || (cm[rc] != 0);
-            if (any) beam_merge<TR, CR>(beam, ck, cm, T, scratch);
+            if (any) beam_merge<TR, CR, false>(beam, ck, cm, T, scratch, merge_aux);
         }
         // flush the K smallest, ascending
         uint32_t* out = p.results + qid * p.K;
@@ -204,20 +208,18 @@ __global__ void __launch_bounds__(512) search_kernel(const SearchParams p) {
         const QuadShape S = p.Q;
         const uint32_t qi = lane & (S.qpn - 1), nl = lane >> S.qshift;
 
-        // quantize the query; the lane's plane words (wave-uniform in the narrow layout)
-        uint32_t pl[6][4];
+        // quantize the query.  Wide layout: the lane's plane words stay in registers;
+        // narrow layout: the 24 words all lanes share stay in LDS (planes4, outside the
+        // merge scratch) and are re-read per expansion.
+        uint4 pl[6];
         QuantOut qo;
+        uint32_t* planes4 = reinterpret_cast<uint32_t*>(my + p.off_planes);
         {
             float* qscr = reinterpret_cast<float*>(scratch);
             uint32_t* planes = reinterpret_cast<uint32_t*>(my + p.off_scratch + 4u * p.pdim);
             qo = quantize(qv, p.signs, p.dim, p.pdim, 0u, qscr, planes, nullptr);
-            lane_plane_quads(planes, wpp, S, pl);
-            if constexpr (!WIDE) {
-#pragma unroll
-                for (int b = 0; b < 6; ++b)
-#pragma unroll
-                    for (int k = 0; k < 4; ++k) pl[b][k] = uniform(pl[b][k]);
-            }
+            if constexpr (WIDE) lane_plane_quads(planes, wpp, S, pl);
+            else store_planes4(planes, wpp, planes4);
         }
         hf.clear();
 
@@ -227,7 +229,7 @@ __global__ void __launch_bounds__(512) search_kernel(const SearchParams p) {
             n_dist = 1;
             uint64_t ck[1] = {lane == 0 ? make_key(d0, p.entry) : EMPTY_KEY};
             uint64_t cm[1] = {1ull};
-            beam_merge<TR, 1>(beam, ck, cm, T, scratch);
+            beam_merge<TR, 1>(beam, ck, cm, T, scratch, merge_aux);
         }
         uint32_t* rawbuf = cand_ids;
 
@@ -284,6 +286,8 @@ __global__ void __launch_bounds__(512) search_kernel(const SearchParams p) {
                 }
             } else {
 #pragma unroll
+                for (int b = 0; b < 6; ++b) pl[b] = reinterpret_cast<const uint4*>(planes4)[b];
+#pragma unroll
                 for (int rc = 0; rc < CR; ++rc) raw[rc] = raw_quad(pl, cw[rc < NC ? rc : 0]);
             }
             uint64_t ck[CR], cm[CR];
@@ -299,7 +303,7 @@ __global__ void __launch_bounds__(512) search_kernel(const SearchParams p) {
             }
             wave_sync();
             n_est += nv;
-            beam_merge<TR, CR>(beam, ck, cm, T, scratch);
+            beam_merge<TR, CR>(beam, ck, cm, T, scratch, merge_aux);
         }
 
         // exact rerank of every beam slot (gpu_search_rabitq.cuh:314-317)

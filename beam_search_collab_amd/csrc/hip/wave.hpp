@@ -35,6 +35,9 @@ __device__ __forceinline__ uint64_t readlane64(uint64_t v, uint32_t l) {
 __device__ __forceinline__ uint32_t uniform(uint32_t v) {
     return static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(v)));
 }
+__device__ __forceinline__ uint64_t uniform64(uint64_t v) {
+    return (static_cast<uint64_t>(uniform(static_cast<uint32_t>(v >> 32))) << 32) | uniform(static_cast<uint32_t>(v));
+}
 
 // Orders LDS traffic of the wave: every lane's earlier LDS writes are visible to every
 // lane's later LDS reads, and the compiler may not move LDS accesses across it.
