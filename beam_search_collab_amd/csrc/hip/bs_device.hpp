@@ -309,6 +309,7 @@ struct HashLds {
     // step, first slot that holds k (present) or is empty (insert there).
     // returns 1 if newly inserted; 0 if present or the table is full.
     __device__ __forceinline__ uint32_t insert1(uint32_t k) {
+        if (occ >= size) return 0u;  // full: present or rejected, 0 either way
         const uint32_t lane = lane_id();
         const uint32_t h = slot0(k);
         for (uint32_t base = 0; base < size; base += 64) {
@@ -351,7 +352,9 @@ struct HashLds {
         const uint64_t vm = ballot(valid);
         const uint32_t nv = static_cast<uint32_t>(__builtin_popcountll(vm));
         uint32_t isnew = 0;
-        if (nv == 0) return 0;
+        // A full table accepts nothing and every key already present reports 0, so the
+        // batch changes nothing (filter_hash.cuh:78-86 probes all slots to the same end).
+        if (nv == 0 || occ >= size) return 0;
         if (occ + nv <= size) {
             uint32_t idx = slot0(k);
             bool done = !valid;
@@ -372,8 +375,9 @@ struct HashLds {
             wave_sync();
             occ += static_cast<uint32_t>(__builtin_popcountll(ballot(isnew != 0)));
         } else {
+            // lane order until the table fills; the keys after that all report 0
             uint64_t m = vm;
-            while (m) {
+            while (m && occ < size) {
                 const uint32_t l = static_cast<uint32_t>(__builtin_ctzll(m));
                 m &= m - 1;
                 const uint32_t r = insert1(readlane(k, l));
