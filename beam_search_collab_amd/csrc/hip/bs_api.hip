@@ -203,7 +203,7 @@ namespace {
 
 struct Plan {
     bsd::SearchParams p;
-    int TR, CR, QMAX, mode;
+    int TR, CR, PB, mode;
     dim3 grid, block;
     size_t lds;
 };
@@ -233,8 +233,8 @@ int make_plan(bs_index ix, const bs_search_cfg* cfg, uint64_t nq, Plan& pl) {
     pl.TR = T <= 64 ? 1 : T <= 128 ? 2 : T <= 256 ? 4 : 8;
     pl.CR = ix->degree <= 64 ? 1 : 2;
     bsd::L2Shape L = bsd::l2_shape(ix->dim);
-    pl.QMAX = 4;
     if (L.QR > 4) return fail(BS_EINVAL, "dim too large");
+    pl.PB = bsd::l2_passes_in_flight(L);
 
     bsd::SearchParams& p = pl.p;
     std::memset(&p, 0, sizeof(p));
@@ -296,11 +296,11 @@ int make_plan(bs_index ix, const bs_search_cfg* cfg, uint64_t nq, Plan& pl) {
 
 hipError_t launch(const Plan& pl, hipStream_t s) {
     switch (pl.mode) {
-    case BS_GROUP_BLOOM: return bsd::launch_search_bloom(pl.p, pl.TR, pl.CR, pl.QMAX, pl.grid, pl.block, pl.lds, s);
+    case BS_GROUP_BLOOM: return bsd::launch_search_bloom(pl.p, pl.TR, pl.CR, pl.PB, pl.grid, pl.block, pl.lds, s);
     case BS_RABITQ:
-        if (pl.p.wpp <= 4) return bsd::launch_search_rabitq(pl.p, pl.TR, pl.CR, pl.QMAX, pl.grid, pl.block, pl.lds, s);
-        return bsd::launch_search_rabitq_wide(pl.p, pl.TR, pl.CR, pl.QMAX, pl.grid, pl.block, pl.lds, s);
-    default: return bsd::launch_search_hash(pl.p, pl.TR, pl.CR, pl.QMAX, pl.grid, pl.block, pl.lds, s);
+        if (pl.p.wpp <= 4) return bsd::launch_search_rabitq(pl.p, pl.TR, pl.CR, pl.PB, pl.grid, pl.block, pl.lds, s);
+        return bsd::launch_search_rabitq_wide(pl.p, pl.TR, pl.CR, pl.PB, pl.grid, pl.block, pl.lds, s);
+    default: return bsd::launch_search_hash(pl.p, pl.TR, pl.CR, pl.PB, pl.grid, pl.block, pl.lds, s);
     }
 }
 

@@ -208,17 +208,22 @@ __device__ __forceinline__ void beam_merge(uint64_t (&beam)[TR], const uint64_t 
 template <int TR, bool RUN>
 __device__ __forceinline__ uint32_t beam_pick(uint64_t (&beam)[TR]) {
     const uint32_t lane = lane_id();
-    int pr = -1;
-    uint32_t pl = 0;
+    uint64_t m[TR];
 #pragma unroll
-    for (int r = 0; r < TR; ++r) {
-        const uint64_t m = ballot((static_cast<uint32_t>(beam[r]) & 1u) == 0u);
-        if (pr < 0 && m != 0) {
+    for (int r = 0; r < TR; ++r) m[r] = ballot((static_cast<uint32_t>(beam[r]) & 1u) == 0u);
+    int pr = -1;
+    uint64_t mp = 0;
+#pragma unroll
+    for (int r = TR - 1; r >= 0; --r) {
+        if (m[r] != 0) {
             pr = r;
-            pl = static_cast<uint32_t>(__builtin_ctzll(m));
+            mp = m[r];
         }
     }
     if (pr < 0) return INVALID;
+    const uint32_t pl = static_cast<uint32_t>(__builtin_ctzll(mp));
+    // (a readlane per candidate register: a select chain over the registers would be
+    // turned into a dynamically indexed array, i.e. scratch memory)
     uint64_t kp = 0;
 #pragma unroll
     for (int r = 0; r < TR; ++r)
@@ -226,18 +231,33 @@ __device__ __forceinline__ uint32_t beam_pick(uint64_t (&beam)[TR]) {
     int qr = pr;
     uint32_t ql = pl;
     if constexpr (RUN) {
+        // identical keys are rare: look at the next element first, scan only if it repeats
+        uint64_t nxt = EMPTY_KEY;
+        const int nr = pl < 63u ? pr : pr + 1;
+        const uint32_t nl = pl < 63u ? pl + 1u : 0u;
 #pragma unroll
-        for (int r = 0; r < TR; ++r) {
-            const uint64_t m = ballot(beam[r] == kp);
-            if (r >= pr && m != 0) {
-                qr = r;
-                ql = 63u - static_cast<uint32_t>(__builtin_clzll(m));
+        for (int r = 0; r < TR; ++r)
+            if (r == nr) nxt = readlane64(beam[r], nl);
+        if (nxt == kp) {
+#pragma unroll
+            for (int r = 0; r < TR; ++r) {
+                const uint64_t mm = ballot(beam[r] == kp);
+                if (r >= pr && mm != 0) {
+                    qr = r;
+                    ql = 63u - static_cast<uint32_t>(__builtin_clzll(mm));
+                }
             }
         }
     }
+    // set the mark (key LSB) of element (qr, ql): only the low word changes
+    const uint32_t bit = (lane == ql) ? 1u : 0u;
 #pragma unroll
-    for (int r = 0; r < TR; ++r)
-        if (r == qr && lane == ql) beam[r] |= 1ull;
+    for (int r = 0; r < TR; ++r) {
+        if (r == qr) {
+            const uint32_t lo = static_cast<uint32_t>(beam[r]) | bit;
+            beam[r] = (beam[r] & 0xFFFFFFFF00000000ull) | lo;
+        }
+    }
     return key_id(kp);
 }
 
@@ -486,6 +506,13 @@ struct L2Shape {
 // (1 <= G <= 64), so each lane holds QR = ceil(chunks/G) <= 4 chunks (for dim <= 1024) and a
 // 64-lane pass covers 64/G rows.  Four chunks per lane keep the butterfly short (log2 G
 // steps per pass) and put 64/G rows of loads in flight per pass.
+// Passes in flight for l2_rows: about 16 rows per batch, 2..8 passes (at most 128 VGPRs
+// of loads; a row of dim > 256 spans 32 or 64 lanes, so one pass holds only 1-2 rows).
+__host__ __device__ inline int l2_passes_in_flight(const L2Shape& L) {
+    const uint32_t pb = 16u / L.rpp;
+    return pb <= 2u ? 2 : pb >= 8u ? 8 : static_cast<int>(pb);
+}
+
 __host__ __device__ inline L2Shape l2_shape(uint32_t dim) {
     L2Shape L;
     L.chunks = (dim + 3) / 4;
@@ -571,15 +598,12 @@ __device__ __forceinline__ void load_query(const float* qv, uint32_t dim, uint32
 }
 
 // Distances of `cnt` rows whose ids are in lds_ids[0..cnt), written to lds_d[0..cnt).
-// Rows are `stride` floats apart.  Passes of rpp rows, PB passes in flight.
-template <int QMAX>
+// Rows are `stride` floats apart.  Passes of rpp rows, PB passes (PB * QMAX float4 loads
+// per lane) in flight before the first reduction.
+template <int QMAX, int PB>
 __device__ __forceinline__ void l2_rows(const float4 (&q)[QMAX], const float* base, uint64_t stride,
                                         const uint32_t* lds_ids, float* lds_d, uint32_t cnt,
                                         const L2Shape& L) {
-#ifndef BS_L2_PASSES_IN_FLIGHT
-#define BS_L2_PASSES_IN_FLIGHT 2
-#endif
-    constexpr int PB = BS_L2_PASSES_IN_FLIGHT;
     const uint32_t lane = lane_id();
     const uint32_t g = lane >> L.gshift, lig = lane & (L.G - 1);
     for (uint32_t j0 = 0; j0 < cnt; j0 += PB * L.rpp) {

@@ -4,13 +4,13 @@
 #include "bs_search.hpp"
 
 namespace bsd {
-// TR in {1,2,4,8}, CR in {1,2}, QMAX = 4
-hipError_t launch_search_hash(const SearchParams& p, int TR, int CR, int QMAX, dim3 grid, dim3 block,
+// TR in {1,2,4,8}, CR in {1,2}, PB (L2 passes in flight) in {2,4,8}
+hipError_t launch_search_hash(const SearchParams& p, int TR, int CR, int PB, dim3 grid, dim3 block,
                               size_t lds, hipStream_t s);
-hipError_t launch_search_bloom(const SearchParams& p, int TR, int CR, int QMAX, dim3 grid, dim3 block,
+hipError_t launch_search_bloom(const SearchParams& p, int TR, int CR, int PB, dim3 grid, dim3 block,
                                size_t lds, hipStream_t s);
-hipError_t launch_search_rabitq(const SearchParams& p, int TR, int CR, int QMAX, dim3 grid, dim3 block,
+hipError_t launch_search_rabitq(const SearchParams& p, int TR, int CR, int PB, dim3 grid, dim3 block,
                                 size_t lds, hipStream_t s);
-hipError_t launch_search_rabitq_wide(const SearchParams& p, int TR, int CR, int QMAX, dim3 grid, dim3 block,
+hipError_t launch_search_rabitq_wide(const SearchParams& p, int TR, int CR, int PB, dim3 grid, dim3 block,
                                      size_t lds, hipStream_t s);
 }  // namespace bsd

@@ -36,7 +36,7 @@ struct SearchParams {
     L2Shape L;
 };
 
-template <int TR, int CR, int QMAX, int MODE>
+template <int TR, int CR, int QMAX, int MODE, int PB>
 __global__ void __launch_bounds__(512) search_kernel(const SearchParams p) {
     extern __shared__ __attribute__((aligned(16))) char smem[];
     const uint32_t lane = lane_id();
@@ -166,7 +166,7 @@ __global__ void __launch_bounds__(512) search_kernel(const SearchParams p) {
             wave_sync();
             if (c == 0) continue;
             n_dist += c;
-            l2_rows<QMAX>(q, vbase, vstride, cand_ids, cand_d, c, L);
+            l2_rows<QMAX, PB>(q, vbase, vstride, cand_ids, cand_d, c, L);
 #pragma unroll
             for (int rc = 0; rc < CR; ++rc) {
                 const uint32_t j = static_cast<uint32_t>(rc) * 64u + lane;
@@ -318,7 +318,7 @@ __global__ void __launch_bounds__(512) search_kernel(const SearchParams p) {
         }
         wave_sync();
         // the valid entries are the first nvb (the beam is sorted, empty keys last)
-        l2_rows<QMAX>(q, rbase, rstride, ids, rd, nvb, L);
+        l2_rows<QMAX, PB>(q, rbase, rstride, ids, rd, nvb, L);
         n_rr += nvb;
 #pragma unroll
         for (int r = 0; r < TR; ++r) {
