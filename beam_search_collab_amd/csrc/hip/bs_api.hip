@@ -58,6 +58,7 @@ struct bs_index_s {
     uint32_t* d_recs = nullptr;
     float* d_signs = nullptr;
     size_t max_lds = 65536;
+    uint32_t cus = 256;  // compute units of the device
 };
 
 extern "C" const char* bs_last_error(void) { return g_err.c_str(); }
@@ -98,6 +99,9 @@ extern "C" int bs_index_create(const float* vecs, const uint32_t* edges, uint64_
     int lds = 0;
     if (hipDeviceGetAttribute(&lds, hipDeviceAttributeMaxSharedMemoryPerBlock, ix->device) == hipSuccess && lds > 0)
         ix->max_lds = static_cast<size_t>(lds);
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, ix->device) == hipSuccess && cus > 0)
+        ix->cus = static_cast<uint32_t>(cus);
     const size_t vbytes = n * ix->dstride * sizeof(float);
     if (hipMalloc(&ix->d_vecs, vbytes) != hipSuccess) {
         delete ix;
@@ -282,12 +286,22 @@ int make_plan(bs_index ix, const bs_search_cfg* cfg, uint64_t nq, Plan& pl) {
     p.off_scratch = al(filter_bytes);
     p.off_cand = p.off_scratch + al(scratch);
     if (mode == BS_RABITQ) p.off_planes += p.off_scratch;
-    p.lds_wave = al(p.off_cand + 64u * pl.CR * 8u + 64u);  // + the merge's slot bitmap
+    p.off_coop = p.off_cand + 64u * pl.CR * 8u + 64u;       // after the merge's slot bitmap
+    p.lds_wave = al(p.off_coop + 4u);
+    // base mode with too few queries to give every SIMD 4 wavefronts: 2 or 4 wavefronts
+    // share one query (the reference's block-per-query base kernel); they split the
+    // distance rows of each expansion, the rest of the loop runs on the first wavefront
+    p.coop = 1;
+    if (mode == BS_BASE) {
+        const uint64_t slots = 16ull * ix->cus;
+        if (nq * 4 <= slots) p.coop = 4;
+        else if (nq * 2 <= slots) p.coop = 2;
+    }
     pl.lds = static_cast<size_t>(p.lds_wave) * ny;
     if (pl.lds > ix->max_lds)
         return fail(BS_EINVAL, "LDS per workgroup " + std::to_string(pl.lds) + " B exceeds the device limit " +
                                    std::to_string(ix->max_lds) + " B (lower filter_capacity or queries_per_group)");
-    pl.block = dim3(64 * ny);
+    pl.block = dim3(64 * (p.coop > 1 ? p.coop : ny));
     const uint64_t groups = (nq + ny - 1) / ny;
     if (groups > 0x7FFFFFFFull) return fail(BS_EINVAL, "too many queries for one launch");
     pl.grid = dim3(static_cast<uint32_t>(groups));

@@ -33,6 +33,8 @@ struct SearchParams {
     uint32_t lds_wave;      // bytes of LDS per wavefront
     uint32_t off_filter, off_scratch, off_cand;  // byte offsets inside the wave slice
     uint32_t off_planes;    // rabitq: the query's bit planes (outside the merge scratch)
+    uint32_t coop;          // base mode: wavefronts per query (1, 2, 4); 1 otherwise
+    uint32_t off_coop;      // word where the first wavefront posts the row count
     L2Shape L;
 };
 
@@ -41,10 +43,12 @@ __global__ void __launch_bounds__(512) search_kernel(const SearchParams p) {
     extern __shared__ __attribute__((aligned(16))) char smem[];
     const uint32_t lane = lane_id();
     const uint32_t wave = threadIdx.x >> 6;
-    const uint64_t qid = static_cast<uint64_t>(blockIdx.x) * (blockDim.x >> 6) + wave;
+    const uint32_t coop = p.coop;  // > 1: the workgroup's wavefronts share one query
+    const uint64_t qid = coop > 1 ? static_cast<uint64_t>(blockIdx.x)
+                                  : static_cast<uint64_t>(blockIdx.x) * (blockDim.x >> 6) + wave;
     if (qid >= p.nq) return;
 
-    char* my = smem + static_cast<size_t>(wave) * p.lds_wave;
+    char* my = smem + static_cast<size_t>(coop > 1 ? 0u : wave) * p.lds_wave;
     uint64_t* scratch = reinterpret_cast<uint64_t*>(my + p.off_scratch);
     uint32_t* cand_ids = reinterpret_cast<uint32_t*>(my + p.off_cand);
     float* cand_d = reinterpret_cast<float*>(my + p.off_cand) + 64 * CR;
@@ -67,6 +71,23 @@ __global__ void __launch_bounds__(512) search_kernel(const SearchParams p) {
 
     if constexpr (MODE == MODE_HASH || MODE == MODE_BLOOM) {
         // ------------------------------------------------------------------ base
+        const float* vbase = p.vecs;
+        const uint64_t vstride = p.dstride;
+        uint32_t* batch = reinterpret_cast<uint32_t*>(my + p.off_coop);
+        if (coop > 1 && wave != 0) {
+            // helper wavefront: wait for a posted batch of candidate ids, compute its
+            // share of their distances, repeat until the first wavefront posts INVALID
+            for (;;) {
+                __syncthreads();
+                const uint32_t c = *batch;
+                if (c == INVALID) break;
+                const uint32_t lo = c * wave / coop, hi = c * (wave + 1) / coop;
+                if (hi > lo) l2_rows<QMAX, PB>(q, vbase, vstride, cand_ids + lo, cand_d + lo, hi - lo, L);
+                __syncthreads();
+            }
+            return;
+        }
+
         HashLds hf;
         BloomLds bf;
         if constexpr (MODE == MODE_HASH) {
@@ -82,9 +103,6 @@ __global__ void __launch_bounds__(512) search_kernel(const SearchParams p) {
             bf.mask = (p.filter_bits >= 32) ? 0xFFFFFFFFu : ((1u << p.filter_bits) - 1);
             bf.clear();
         }
-        const float* vbase = p.vecs;
-        const uint64_t vstride = p.dstride;
-
         // seed: the entry point is the only candidate (gpu_search_base.cuh:142-152)
         uint64_t ck[CR];
         uint64_t cm[CR];
@@ -166,7 +184,15 @@ __global__ void __launch_bounds__(512) search_kernel(const SearchParams p) {
             wave_sync();
             if (c == 0) continue;
             n_dist += c;
-            l2_rows<QMAX, PB>(q, vbase, vstride, cand_ids, cand_d, c, L);
+            if (coop > 1) {
+                if (lane == 0) *batch = c;
+                __syncthreads();  // batch posted
+                const uint32_t hi = c / coop;
+                if (hi > 0) l2_rows<QMAX, PB>(q, vbase, vstride, cand_ids, cand_d, hi, L);
+                __syncthreads();  // every share of cand_d written
+            } else {
+                l2_rows<QMAX, PB>(q, vbase, vstride, cand_ids, cand_d, c, L);
+            }
 #pragma unroll
             for (int rc = 0; rc < CR; ++rc) {
                 const uint32_t j = static_cast<uint32_t>(rc) * 64u + lane;
@@ -175,6 +201,10 @@ __global__ void __launch_bounds__(512) search_kernel(const SearchParams p) {
                 cm[rc] = ballot(v);
             }
             wave_sync();
+        }
+        if (coop > 1) {  // release the helper wavefronts
+            if (lane == 0) *batch = INVALID;
+            __syncthreads();
         }
         {
             bool any = false;
