@@ -63,7 +63,8 @@ def test_modes_topk_d128(gpu, mode, topk):
 
 
 @pytest.mark.parametrize("dim,degree,kind", [(32, 16, "mixture"), (100, 64, "normalized"), (64, 100, "normalized"),
-                                             (960, 32, "mixture"), (25, 24, "normalized"), (200, 48, "mixture")])
+                                             (960, 32, "mixture"), (25, 24, "normalized"), (200, 48, "mixture"),
+                                             (300, 32, "mixture")])
 @pytest.mark.parametrize("mode", ["warp1", "bwarp2", "rabitq"])
 def test_shapes(gpu, dim, degree, kind, mode):
     if mode == "rabitq" and dim < 17:
@@ -101,6 +102,19 @@ def test_group_modes_identical_and_deterministic(gpu):
             if ref is None:
                 ref = ids
             assert np.array_equal(ids, ref), m
+
+
+@pytest.mark.parametrize("nq", [700, 1500, 3000])
+def test_base_waves_per_query(gpu, nq):
+    """base mode gives a query 4, 2 or 1 wavefronts depending on how many queries the launch
+    has (nq * 4 <= 16 * CUs, nq * 2 <= 16 * CUs, else 1 on a 256-CU MI355X): the split of a
+    candidate batch over wavefronts must not change any result or counter"""
+    ds = dataset(3000, 64, 32, nq)
+    for topk in (64, 256):
+        assert_same(*run_both(ds, "base", 10, topk), f"base nq={nq} topk={topk}")
+        ids_w, _, _ = ds["g"].search(ds["q"], 10, "warp1", GPUBaseSearchCfg(topk, 1024, ds["entry"], 1024, 16))
+        ids_b, _, _ = ds["g"].search(ds["q"], 10, "base", GPUBaseSearchCfg(topk, 1024, ds["entry"], 1024, 16))
+        assert np.array_equal(ids_w, ids_b)
 
 
 def test_k_equals_topk_and_empty_results(gpu):
