@@ -73,6 +73,7 @@ class GPUGraph:
             raise ValueError("vecs must be n x dim and edges n x degree")
         self.n, self.dim = vecs.shape
         self.degree = edges.shape[1]
+        self._vecs = vecs  # host rows, for the exact fallback of groundtruth()
         self.padded_dim = 0
         h = C.c_void_p()
         _check(_lib.hip().bs_index_create(_ptr(vecs), _ptr(edges), self.n, self.dim, self.degree, C.byref(h)),
@@ -122,6 +123,29 @@ class GPUGraph:
         _check(_lib.hip().bs_search(self._h, C.byref(c), _ptr(q), nq, _ptr(res),
                                     _ptr(d) if d is not None else None, C.byref(st)), "bs_search")
         return res, d, st.as_dict()
+
+    def groundtruth(self, queries: np.ndarray, k: int = 100, exact_fallback: bool = True) -> np.ndarray:
+        """Exact k nearest rows (int32, -1 past the last row) by fp64 distance, ties by id.
+        Matrix-core candidates with a per-query certificate; the queries without one are
+        recomputed on the host (bs_groundtruth) unless exact_fallback is False, in which
+        case their rows are -2."""
+        q = np.ascontiguousarray(queries, dtype=np.float32)
+        if q.ndim != 2 or q.shape[1] != self.dim:
+            raise ValueError(f"queries must be nq x {self.dim}")
+        nq = q.shape[0]
+        out = np.empty((nq, k), dtype=np.int32)
+        unc = np.zeros(nq, dtype=np.uint8)
+        nu = C.c_uint64(0)
+        _check(_lib.hip().bs_index_groundtruth(self._h, _ptr(q), nq, k, _ptr(out), _ptr(unc), C.byref(nu)),
+               "bs_index_groundtruth")
+        bad = np.nonzero(unc)[0]
+        if len(bad):
+            if exact_fallback:
+                from . import host
+                out[bad] = host.groundtruth(self._vecs, q[bad], k)
+            else:
+                out[bad] = -2
+        return out
 
     def search_device(self, d_queries: int, nq: int, d_results: int, K: int, mode: str, cfg,
                       d_dists: int = 0, d_per_query: int = 0, stream: int = 0, sync: bool = False) -> dict:
@@ -209,6 +233,14 @@ def debug_sort(keys):
     out = np.empty_like(keys)
     _check(_lib.hip().bs_debug_sort(_ptr(keys), keys.shape[0], _ptr(out)), "bs_debug_sort")
     return out
+
+
+def debug_mfma32(A, B):
+    A = np.ascontiguousarray(A, dtype=np.float32).reshape(32, 2)
+    B = np.ascontiguousarray(B, dtype=np.float32).reshape(2, 32)
+    D = np.empty((32, 32), dtype=np.float32)
+    _check(_lib.hip().bs_debug_mfma32(_ptr(A), _ptr(B), _ptr(D)), "bs_debug_mfma32")
+    return D
 
 
 def debug_filter(bloom, capacity, keys, qkeys):

@@ -111,6 +111,23 @@ int bs_index_info(bs_index idx, uint64_t* n, uint32_t* dim, uint32_t* degree,
 void bs_index_destroy(bs_index idx);
 const char* bs_last_error(void);
 
+/* ---- exact ground truth (no counterpart in the reference, whose ground truth comes from
+ * HDF5 files, script/unpack.py:56-81) ---------------------------------------------------
+ * The k nearest rows of the index (k <= 128, dim <= 256) to each of nq queries by exact
+ * distance: fp64 squared differences summed in dimension order, ties by id -- the order of
+ * bs_groundtruth (bs_host.h).  Candidates come from fp32 matrix-core dot products; each
+ * query carries a certificate that no row outside its candidates can be among the k nearest.
+ * out: nq*k int32 (-1 where fewer than k rows exist).  uncertified: nq bytes (1 = no
+ * certificate: recompute that query, e.g. with bs_groundtruth) or NULL; n_uncertified
+ * (nullable) gets their number.  Synchronous; allocates device work buffers. */
+int bs_index_groundtruth(bs_index idx, const float* queries, uint64_t nq, uint32_t k, int32_t* out,
+                         uint8_t* uncertified, uint64_t* n_uncertified);
+/* The same on device buffers (queries nq*dim f32, out nq*k int32, uncertified nq u8 or
+ * NULL), launched on `stream` (hipStream_t or NULL), synchronous at return. */
+int bs_index_groundtruth_device(bs_index idx, const float* d_queries, uint64_t nq, uint32_t k,
+                                int32_t* d_out, uint8_t* d_uncertified, void* stream,
+                                uint64_t* n_uncertified);
+
 /* ---- primitive entry points (parity tests of the device building blocks) ----------
  * Each runs the same device functions the search kernels use, on one wavefront per
  * instance.  All buffers are host memory. */
@@ -142,6 +159,10 @@ int bs_debug_beam(uint32_t topk, const uint64_t* keys, uint32_t nbatch, uint32_t
 /* Full sort of n (<= 512) keys ascending (the rerank sorter; replaces the bitonic
  * re-sort of topk_shared.cuh:384-416). */
 int bs_debug_sort(const uint64_t* keys, uint32_t n, uint64_t* out);
+
+/* One v_mfma_f32_32x32x2f32 product: A 32x2 and B 2x32 row-major in, D = A B 32x32
+ * row-major out, read back through the accumulator layout the ground-truth kernel uses. */
+int bs_debug_mfma32(const float* A, const float* B, float* D);
 
 /* Visit filters: nbatch lane-parallel batches of bsize (<= 64) inserts (0xFFFFFFFF =
  * idle lane), then nquery contains().  bloom = 0: HashFilter (filter_hash.cuh),

@@ -1,0 +1,48 @@
+"""Exact ground truth on the matrix cores against the host's fp64 brute force (bs_groundtruth):
+identical ids (distance, then id order), certificates present for all but a few queries."""
+import numpy as np
+import pytest
+
+from beam_search_collab_amd import host, search
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("n,dim,kind,k", [(20000, 128, "mixture", 100), (15000, 100, "normalized", 10),
+                                          (12000, 32, "mixture", 128), (9000, 200, "normalized", 50),
+                                          (5000, 256, "mixture", 1), (150, 64, "normalized", 100),
+                                          (90, 17, "mixture", 100)])
+def test_groundtruth_matches_host(gpu, n, dim, kind, k):
+    if kind == "mixture":
+        base = host.gen_mixture(n, dim, 16, 0.0, 128.0, 12.0, 0.0, 11, 12)
+        q = host.gen_mixture(300, dim, 16, 0.0, 128.0, 12.0, 0.0, 11, 13)
+    else:
+        base = host.gen_normalized(n, dim, 12)
+        q = host.gen_normalized(300, dim, 13)
+    edges = np.zeros((n, 4), np.uint32)
+    g = search.GPUGraph(base, edges)
+    exact = host.groundtruth(base, q, k)
+    raw = g.groundtruth(q, k, exact_fallback=False)
+    certified = (raw != -2).all(1)
+    # 128 candidates per query: the certificate needs some of them beyond the k-th
+    if k <= 100:
+        assert certified.mean() >= 0.95, certified.mean()
+    assert np.array_equal(raw[certified], exact[certified])
+    assert np.array_equal(g.groundtruth(q, k), exact)
+
+
+def test_groundtruth_duplicates_and_ties(gpu):
+    # repeated rows: equal distances must come out in id order
+    rng = np.random.default_rng(7)
+    uniq = rng.integers(0, 4, (500, 64)).astype(np.float32)
+    base = np.concatenate([uniq, uniq, uniq])
+    q = rng.integers(0, 4, (64, 64)).astype(np.float32)
+    g = search.GPUGraph(base, np.zeros((base.shape[0], 2), np.uint32))
+    assert np.array_equal(g.groundtruth(q, 100), host.groundtruth(base, q, 100))
+
+
+def test_groundtruth_rejects_large_dim(gpu):
+    base = host.gen_normalized(1000, 300, 1)
+    g = search.GPUGraph(base, np.zeros((1000, 2), np.uint32))
+    with pytest.raises(ValueError):
+        g.groundtruth(base[:4], 10)

@@ -127,3 +127,13 @@ def test_host_tools_do_not_need_the_gpu_but_index_does(gpu):
     base = host.gen_normalized(64, 8, 1)
     with pytest.raises(ValueError):
         search.GPUGraph(base, np.full((64, 4), 64, np.uint32))  # edge out of range
+
+
+def test_mfma32_layout(gpu):
+    """the accumulator layout the ground-truth kernel reads back (row 8(r/4)+4(lane/32)+r%4,
+    column lane%32 for register r) gives D = A B for one v_mfma_f32_32x32x2f32"""
+    rng = np.random.default_rng(3)
+    A = rng.integers(-8, 8, (32, 2)).astype(np.float32)
+    B = rng.integers(-8, 8, (2, 32)).astype(np.float32)
+    D = search.debug_mfma32(A, B)
+    assert np.array_equal(D, A @ B)
