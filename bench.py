@@ -93,7 +93,8 @@ def gen_data(args):
 
 
 def gt_gpu(base_t, q_t, k, margin=28):
-    """exact top-k (fp64 distances, ties by id, as bs_groundtruth): fp32 GEMM candidates
+    """exact top-k for dim > 256 (beyond bs_index_groundtruth), fp64 distances, ties by id
+    as bs_groundtruth: fp32 library-GEMM candidates
     on the GPU, exact fp64 re-scoring on the host, and a per-query certificate.
 
     Candidate a_j = |b_j|^2 - 2 q.b_j (+ |q|^2) in fp32 differs from the exact distance by
@@ -301,11 +302,15 @@ def main():
         edges = host.build_vamana(base, args.degree, 128, 2.0, 1234, exact=False, verbose=True)
         log(f"Vamana graph R={args.degree}: {time.time() - t1:.1f}s")
         t1 = time.time()
-        base_t = torch.from_numpy(base).to(dev)
         q_t = torch.from_numpy(queries).to(dev)
-        gt = gt_gpu(base_t, q_t, 100)
-        del base_t
-        torch.cuda.empty_cache()
+        if args.dim <= 256:
+            # matrix-core brute force with per-query certificates (bs_index_groundtruth)
+            gt = search.GPUGraph(base, edges).groundtruth(queries, 100)
+        else:
+            base_t = torch.from_numpy(base).to(dev)
+            gt = gt_gpu(base_t, q_t, 100)
+            del base_t
+            torch.cuda.empty_cache()
         log(f"ground truth top-100: {time.time() - t1:.1f}s")
         if cache:
             os.makedirs(args.cache, exist_ok=True)
