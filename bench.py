@@ -238,13 +238,21 @@ def cpu_baseline(files, nq_total, args):
             "sample": f"{per} queries, CPU oracle restatement of the reference cpu_cli {cli_mode} search, one thread"}
 
 
-def kernel_name(mode, topk, degree):
+def kernel_name(mode, topk, degree, dim):
     """symbol of the search-kernel instance a launch uses (beam registers TR = topk/64,
-    candidate registers CR = degree/64, 4 float4 chunks per lane, filter/mode id)"""
+    candidate registers CR = degree/64, 4 float4 chunks per lane, filter/mode id, row
+    passes in flight PB from the L2 row shape)"""
     tr = 1 if topk <= 64 else 2 if topk <= 128 else 4 if topk <= 256 else 8
     cr = 1 if degree <= 64 else 2
     m = {"base": 0, "warp": 0, "bwarp": 1, "rabitq": 2}[mode.rstrip("0123456789")]
-    return f"bsd::search_kernel<{tr}, {cr}, 4, {m}>"
+    p = 1
+    while p < (dim + 3) // 4:
+        p *= 2
+    g = min(max(p // 4, 1), 64)
+    pb = min(max(16 // (64 // g), 2), 8)
+    if m == 2 and dim > 128:
+        m = 3  # rabitq with wide codes (pdim > 128)
+    return f"bsd::search_kernel<{tr}, {cr}, 4, {m}, {pb}>"
 
 
 def measured_traffic(args):
@@ -441,7 +449,7 @@ def main():
                    "expansions_per_query": round(E / nq, 2), "dist_evals_per_query": round(D / nq, 2)},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
-                     "kernel": kernel_name(args.mode, args.topk, R), "avg_launch_ms": round(avg_kernel_ms, 3),
+                     "kernel": kernel_name(args.mode, args.topk, R, d), "avg_launch_ms": round(avg_kernel_ms, 3),
                      "bytes_per_launch": bytes_launch},
         "cpu_baseline": cpu,
     }
