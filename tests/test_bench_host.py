@@ -1,0 +1,35 @@
+"""Host-side logic of bench.py: the byte model, the kernel-instance name it reports and the
+configuration table (no GPU)."""
+import numpy as np
+
+import bench
+
+
+def test_algorithmic_bytes_base_and_rabitq():
+    # per-query counters: iterations, expansions E, exact distances D, estimates, reranks T_r
+    pq = np.array([[10, 8, 100, 0, 0], [5, 4, 50, 0, 0]], dtype=np.int64)
+    d, R, K = 128, 32, 10
+    assert bench.algorithmic_bytes("base", 2, d, R, K, pq) == 2 * (4 * d + 4 * K) + 12 * 4 * R + 150 * 4 * d
+    pr = np.array([[10, 8, 9, 240, 256]], dtype=np.int64)
+    pdim, wpp = 128, 4
+    want = (4 * d + 4 * pdim + 4 * K) + 8 * (4 * R + 4 * R * wpp + 12 * R) + (9 + 256) * 4 * d
+    assert bench.algorithmic_bytes("rabitq", 1, d, R, K, pr, pdim) == want
+
+
+def test_kernel_name_matches_instance_rules():
+    # TR = topk/64 (1,2,4,8), CR = degree/64, PB from the row shape (2 up to dim 128, 4 up to
+    # 256, 8 above), rabitq with pdim > 128 uses the wide instance (mode 3)
+    assert bench.kernel_name("base", 256, 32, 128) == "bsd::search_kernel<4, 1, 4, 0, 2>"
+    assert bench.kernel_name("warp2", 64, 100, 100) == "bsd::search_kernel<1, 2, 4, 0, 2>"
+    assert bench.kernel_name("bwarp1", 128, 64, 200) == "bsd::search_kernel<2, 1, 4, 1, 4>"
+    assert bench.kernel_name("base", 512, 32, 960) == "bsd::search_kernel<8, 1, 4, 0, 8>"
+    assert bench.kernel_name("rabitq", 256, 32, 128) == "bsd::search_kernel<4, 1, 4, 2, 2>"
+    assert bench.kernel_name("rabitq", 256, 32, 960) == "bsd::search_kernel<4, 1, 4, 3, 8>"
+
+
+def test_configs_follow_the_survey():
+    c = bench.CONFIGS
+    assert (c["B"]["n"], c["B"]["dim"], c["B"]["degree"], c["B"]["topk"], c["B"]["K"]) == (1_000_000, 128, 32, 256, 100)
+    assert c["C"]["mode"] == "rabitq" and c["C"]["K"] == 10
+    assert (c["D"]["n"], c["D"]["dim"], c["D"]["degree"], c["D"]["data"]) == (1_200_000, 100, 64, "normal")
+    assert (c["E"]["dim"], c["E"]["nq"], c["E"]["data"]) == (960, 1_000, "mix256")
