@@ -219,7 +219,7 @@ int make_plan(bs_index ix, const bs_search_cfg* cfg, uint64_t nq, Plan& pl) {
     if (mode < BS_BASE || mode > BS_RABITQ) return fail(BS_EINVAL, "unknown mode " + std::to_string(mode));
     if (mode == BS_RABITQ && !ix->d_recs) return fail(BS_EINVAL, "rabitq mode needs bs_index_attach_rabitq first");
     const uint32_t T = cfg->topk_size;
-    if (T == 0 || T > 512) return fail(BS_EINVAL, "topk_size must be in 1..512");
+    if (T == 0 || T > 1024) return fail(BS_EINVAL, "topk_size must be in 1..1024");
     if (cfg->K == 0) return fail(BS_EINVAL, "K must be >= 1");
     if (mode != BS_RABITQ && T < cfg->K)
         return fail(BS_EINVAL, "topk_size (" + std::to_string(T) + ") must be >= K (" + std::to_string(cfg->K) + ")");
@@ -234,7 +234,7 @@ int make_plan(bs_index ix, const bs_search_cfg* cfg, uint64_t nq, Plan& pl) {
     if (cap > (1u << 22)) return fail(BS_EINVAL, "filter_capacity must be <= 2^22");
 
     pl.mode = mode;
-    pl.TR = T <= 64 ? 1 : T <= 128 ? 2 : T <= 256 ? 4 : 8;
+    pl.TR = T <= 64 ? 1 : T <= 128 ? 2 : T <= 256 ? 4 : T <= 512 ? 8 : 16;
     pl.CR = ix->degree <= 64 ? 1 : 2;
     bsd::L2Shape L = bsd::l2_shape(ix->dim);
     if (L.QR > 4) return fail(BS_EINVAL, "dim too large");
@@ -286,7 +286,7 @@ int make_plan(bs_index ix, const bs_search_cfg* cfg, uint64_t nq, Plan& pl) {
     p.off_scratch = al(filter_bytes);
     p.off_cand = p.off_scratch + al(scratch);
     if (mode == BS_RABITQ) p.off_planes += p.off_scratch;
-    p.off_coop = p.off_cand + 64u * pl.CR * 8u + 64u;       // after the merge's slot bitmap
+    p.off_coop = p.off_cand + 64u * pl.CR * 8u + 8u * std::max(pl.TR, 8);  // after the merge's slot bitmap
     p.lds_wave = al(p.off_coop + 4u);
     // base mode with too few queries to give every SIMD 4 wavefronts: 2 or 4 wavefronts
     // share one query (the reference's block-per-query base kernel); they split the

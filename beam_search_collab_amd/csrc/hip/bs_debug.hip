@@ -224,7 +224,7 @@ __global__ void __launch_bounds__(64) dbg_beam_kernel(uint32_t T, const uint64_t
 template <int TR, int CR>
 static void launch_beam(int run, uint32_t T, const uint64_t* k, uint32_t nb, uint32_t bs, uint32_t picks,
                         uint32_t* pk, uint64_t* bo) {
-    const size_t lds = 512u * TR + 8u * (64u + 8u);  // merge scratch + aux
+    const size_t lds = 512u * TR + 8u * (64u + (TR > 8 ? TR : 8));  // merge scratch + aux
     if (run)
         hipLaunchKernelGGL((dbg_beam_kernel<TR, CR, true>), dim3(1), dim3(64), lds, nullptr, T, k, nb, bs, picks, pk, bo);
     else
@@ -241,7 +241,7 @@ static void launch_beam_c(int CR, int run, uint32_t T, const uint64_t* k, uint32
 
 extern "C" int bs_debug_beam(uint32_t topk, const uint64_t* keys, uint32_t nbatch, uint32_t bsize, uint32_t picks,
                              int pick_run, uint32_t* picked, uint64_t* beam_out) {
-    if (topk == 0 || topk > 512) return dfail(BS_EINVAL, "topk must be in 1..512");
+    if (topk == 0 || topk > 1024) return dfail(BS_EINVAL, "topk must be in 1..1024");
     if (bsize == 0 || bsize > 128) return dfail(BS_EINVAL, "bsize must be in 1..128");
     DevBuf<uint64_t> dk, db;
     DevBuf<uint32_t> dp;
@@ -250,13 +250,14 @@ extern "C" int bs_debug_beam(uint32_t topk, const uint64_t* keys, uint32_t nbatc
     DTRY(db.alloc(topk));
     DTRY(dp.alloc(static_cast<size_t>(nbatch) * picks));
     if (nk) DTRY(hipMemcpy(dk.p, keys, nk * 8, hipMemcpyHostToDevice));
-    const int TR = topk <= 64 ? 1 : topk <= 128 ? 2 : topk <= 256 ? 4 : 8;
+    const int TR = topk <= 64 ? 1 : topk <= 128 ? 2 : topk <= 256 ? 4 : topk <= 512 ? 8 : 16;
     const int CR = bsize <= 64 ? 1 : 2;
     switch (TR) {
     case 1: launch_beam_c<1>(CR, pick_run, topk, dk.p, nbatch, bsize, picks, dp.p, db.p); break;
     case 2: launch_beam_c<2>(CR, pick_run, topk, dk.p, nbatch, bsize, picks, dp.p, db.p); break;
     case 4: launch_beam_c<4>(CR, pick_run, topk, dk.p, nbatch, bsize, picks, dp.p, db.p); break;
-    default: launch_beam_c<8>(CR, pick_run, topk, dk.p, nbatch, bsize, picks, dp.p, db.p); break;
+    case 8: launch_beam_c<8>(CR, pick_run, topk, dk.p, nbatch, bsize, picks, dp.p, db.p); break;
+    default: launch_beam_c<16>(CR, pick_run, topk, dk.p, nbatch, bsize, picks, dp.p, db.p); break;
     }
     DTRY(hipGetLastError());
     DTRY(hipMemcpy(beam_out, db.p, topk * 8, hipMemcpyDeviceToHost));
@@ -286,7 +287,7 @@ __global__ void __launch_bounds__(64) dbg_sort_kernel(const uint64_t* keys, uint
 
 extern "C" int bs_debug_sort(const uint64_t* keys, uint32_t n, uint64_t* out) {
     if (n == 0) return BS_OK;
-    if (n > 512) return dfail(BS_EINVAL, "n must be <= 512");
+    if (n > 1024) return dfail(BS_EINVAL, "n must be <= 1024");
     DevBuf<uint64_t> dk, dout;
     DTRY(dk.alloc(n));
     DTRY(dout.alloc(n));
@@ -294,7 +295,8 @@ extern "C" int bs_debug_sort(const uint64_t* keys, uint32_t n, uint64_t* out) {
     if (n <= 64) hipLaunchKernelGGL(dbg_sort_kernel<1>, dim3(1), dim3(64), 0, nullptr, dk.p, n, dout.p);
     else if (n <= 128) hipLaunchKernelGGL(dbg_sort_kernel<2>, dim3(1), dim3(64), 0, nullptr, dk.p, n, dout.p);
     else if (n <= 256) hipLaunchKernelGGL(dbg_sort_kernel<4>, dim3(1), dim3(64), 0, nullptr, dk.p, n, dout.p);
-    else hipLaunchKernelGGL(dbg_sort_kernel<8>, dim3(1), dim3(64), 0, nullptr, dk.p, n, dout.p);
+    else if (n <= 512) hipLaunchKernelGGL(dbg_sort_kernel<8>, dim3(1), dim3(64), 0, nullptr, dk.p, n, dout.p);
+    else hipLaunchKernelGGL(dbg_sort_kernel<16>, dim3(1), dim3(64), 0, nullptr, dk.p, n, dout.p);
     DTRY(hipGetLastError());
     DTRY(hipMemcpy(out, dout.p, n * 8, hipMemcpyDeviceToHost));
     return BS_OK;

@@ -71,7 +71,9 @@ __global__ void __launch_bounds__(256) gt_select(const float* vecs, uint32_t dst
     const uint64_t w = static_cast<uint64_t>(blockIdx.x) * 4 + wave;
     const uint64_t nqb = (nq + 31) / 32;
     if (w >= nqb * nsplit) return;
-    const uint64_t qb = w / nsplit, s = w % nsplit;
+    // consecutive wavefronts take consecutive query blocks of the same row split, so the
+    // wavefronts resident together stream the same base tiles and share them through L2
+    const uint64_t qb = w % nqb, s = w / nqb;
     const uint64_t r0 = s * split_rows;
     const uint64_t r1 = std::min<uint64_t>(n, r0 + split_rows);
 

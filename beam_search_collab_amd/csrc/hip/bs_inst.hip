@@ -50,7 +50,8 @@ static hipError_t launch_any(const SearchParams& p, int TR, int CR, int PB, dim3
     case 1: return launch_c<1>(p, CR, PB, g, b, lds, s);
     case 2: return launch_c<2>(p, CR, PB, g, b, lds, s);
     case 4: return launch_c<4>(p, CR, PB, g, b, lds, s);
-    default: return launch_c<8>(p, CR, PB, g, b, lds, s);
+    case 8: return launch_c<8>(p, CR, PB, g, b, lds, s);
+    default: return launch_c<16>(p, CR, PB, g, b, lds, s);
     }
 }
 

@@ -4,7 +4,7 @@
 #include "bs_search.hpp"
 
 namespace bsd {
-// TR in {1,2,4,8}, CR in {1,2}, PB (L2 passes in flight) in {2,4,8}
+// TR in {1,2,4,8,16}, CR in {1,2}, PB (L2 passes in flight) in {2,4,8}
 hipError_t launch_search_hash(const SearchParams& p, int TR, int CR, int PB, dim3 grid, dim3 block,
                               size_t lds, hipStream_t s);
 hipError_t launch_search_bloom(const SearchParams& p, int TR, int CR, int PB, dim3 grid, dim3 block,

@@ -53,7 +53,7 @@ __global__ void __launch_bounds__(512) search_kernel(const SearchParams p) {
     uint32_t* cand_ids = reinterpret_cast<uint32_t*>(my + p.off_cand);
     float* cand_d = reinterpret_cast<float*>(my + p.off_cand) + 64 * CR;
     // the merge's sorted candidates and slot bitmap reuse the candidate staging area
-    // (free once the keys are in registers), which has room for 64*CR + 8 keys
+    // (free once the keys are in registers), which has room for 64*CR + max(TR, 8) keys
     uint64_t* merge_aux = reinterpret_cast<uint64_t*>(my + p.off_cand);
 
     const L2Shape L = p.L;

@@ -57,7 +57,7 @@ typedef struct {
     int32_t mode;               /* bs_mode                                             */
     uint32_t queries_per_group; /* wavefronts (queries) per workgroup: 1,2,4,8; 0 -> 1  */
     uint32_t K;                 /* results per query (>= 1, <= topk_size)              */
-    uint32_t topk_size;         /* beam slots, 1..512                                  */
+    uint32_t topk_size;         /* beam slots, 1..1024                                 */
     uint32_t filter_capacity;   /* hash slots / Bloom bits (rounded up to a power of 2)*/
     uint32_t entry_point;       /* start node (< n)                                    */
     int32_t max_iterations;     /* >= 0                                                */
@@ -156,7 +156,7 @@ int bs_debug_fastscan(const float* query, const float* signs, uint32_t dim, uint
 int bs_debug_beam(uint32_t topk, const uint64_t* keys, uint32_t nbatch, uint32_t bsize,
                   uint32_t picks, int pick_run, uint32_t* picked, uint64_t* beam_out);
 
-/* Full sort of n (<= 512) keys ascending (the rerank sorter; replaces the bitonic
+/* Full sort of n (<= 1024) keys ascending (the rerank sorter; replaces the bitonic
  * re-sort of topk_shared.cuh:384-416). */
 int bs_debug_sort(const uint64_t* keys, uint32_t n, uint64_t* out);
 

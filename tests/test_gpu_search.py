@@ -55,7 +55,7 @@ def assert_same(ids, d, st, oids, od, ost, ctx):
 
 
 @pytest.mark.parametrize("mode", ["base", "warp1", "warp2", "warp4", "warp8", "bwarp1", "bwarp4", "rabitq"])
-@pytest.mark.parametrize("topk", [16, 64, 100, 128, 256, 512])
+@pytest.mark.parametrize("topk", [16, 64, 100, 128, 256, 512, 1024])
 def test_modes_topk_d128(gpu, mode, topk):
     ds = dataset(4000, 128, 32, 64)
     K = min(10, topk)
@@ -142,7 +142,7 @@ def test_config_errors(gpu):
     with pytest.raises(ValueError):
         g.search(ds["q"], 10, "base", GPUBaseSearchCfg(64, 1024, 10**6, 1024, 16))  # entry out of range
     with pytest.raises(ValueError):
-        g.search(ds["q"], 10, "base", GPUBaseSearchCfg(1024, 1024, 0, 1024, 16))  # topk > 512
+        g.search(ds["q"], 10, "base", GPUBaseSearchCfg(1025, 1024, 0, 1024, 16))  # topk > 1024
     g2 = search.GPUGraph(ds["base"], ds["edges"])
     with pytest.raises(ValueError):
         g2.search(ds["q"], 10, "rabitq")  # no codebook attached
