@@ -57,7 +57,7 @@ __device__ __forceinline__ uint32_t key_id(uint64_t k) { return static_cast<uint
 // first.  Two ways to the same result:
 //  - rank loop: each remaining candidate is broadcast once and compared with every beam
 //    register, ~(3*TR+6) instructions per candidate (few candidates);
-//  - sorted merge (CR = 1, SORTED, at least BS_MERGE_SORT_MIN candidates): the candidates are
+//  - sorted merge (CR = 1, SORTED, at least merge_sort_min<TR>() candidates): the candidates are
 //    compacted and bitonic-sorted across lanes, each finds its rank in the beam by a
 //    binary search of an LDS copy, the occupied output slots are marked in a bitmap and
 //    every output slot gathers its key from the candidate or the beam copy.
@@ -66,9 +66,12 @@ __device__ __forceinline__ uint32_t key_id(uint64_t k) { return static_cast<uint
 // the occupancy limit (the RaBitQ loop); the base loop keeps the rank loop only.
 // LDS: scratch = 64*TR keys, aux = 64 + TR keys.
 // ---------------------------------------------------------------------------
-#ifndef BS_MERGE_SORT_MIN
-#define BS_MERGE_SORT_MIN 8
-#endif
+// The rank loop costs ~(9 + 2 TR) instructions per candidate, the sorted merge a roughly
+// fixed ~250 plus LDS latency: the crossover falls with the beam size.
+template <int TR>
+__device__ __forceinline__ constexpr uint32_t merge_sort_min() {
+    return TR >= 16 ? 3u : TR >= 8 ? 5u : 8u;
+}
 
 // ascending bitonic sort of the first P = pow2ceil(n) lanes (lanes beyond hold EMPTY)
 __device__ __forceinline__ uint64_t sort_lanes(uint64_t v, uint32_t n) {
@@ -149,7 +152,7 @@ __device__ __forceinline__ void beam_merge(uint64_t (&beam)[TR], const uint64_t 
     }
     if (n == 0) return;
     if constexpr (CR == 1 && SORTED) {
-        if (n >= BS_MERGE_SORT_MIN) {
+        if (n >= merge_sort_min<TR>()) {
             beam_merge_sorted<TR>(beam, ck[0], cmask[0], n, T, lds_scratch, lds_aux);
             return;
         }
