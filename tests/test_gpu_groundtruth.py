@@ -46,3 +46,16 @@ def test_groundtruth_rejects_large_dim(gpu):
     g = search.GPUGraph(base, np.zeros((1000, 2), np.uint32))
     with pytest.raises(ValueError):
         g.groundtruth(base[:4], 10)
+
+
+def test_groundtruth_at_scale(gpu):
+    """200k rows, 128 dims: the split lists (many row splits per query block) still give the
+    host brute force's ids for every certified query"""
+    base = host.gen_mixture(200000, 128, 64, 0.0, 128.0, 12.0, 0.0, 101, 202)
+    q = host.gen_mixture(64, 128, 64, 0.0, 128.0, 12.0, 0.0, 101, 303)
+    g = search.GPUGraph(base, np.zeros((200000, 1), np.uint32))
+    raw = g.groundtruth(q, 100, exact_fallback=False)
+    exact = host.groundtruth(base, q, 100)
+    cert = (raw != -2).all(1)
+    assert cert.mean() >= 0.95
+    assert np.array_equal(raw[cert], exact[cert])
