@@ -89,14 +89,21 @@ __global__ void __launch_bounds__(256) gt_select(const float* vecs, uint32_t dst
         const uint64_t qi = qb * 32 + l32;
         const float* qv = queries + std::min<uint64_t>(qi, nq - 1) * dim;
 #pragma unroll
+        for (int t = 0; t < H; ++t) {  // all loads first (clamped), then the zeroing
+            const uint32_t d = half * H + static_cast<uint32_t>(t);
+            a[t] = qv[d < dim ? d : 0u];
+        }
+#pragma unroll
         for (int t = 0; t < H; ++t) {
             const uint32_t d = half * H + static_cast<uint32_t>(t);
-            a[t] = (qi < nq && d < dim) ? qv[d] : 0.0f;
+            if (qi >= nq || d >= dim) a[t] = 0.0f;
         }
     }
-    uint32_t tau[16];
+    // per accumulator register, the threshold of its query: the largest value its list
+    // keeps (a float compare passes a superset of the list's key order)
+    float tau[16];
 #pragma unroll
-    for (int r = 0; r < 16; ++r) tau[r] = 0xFFFFFFFFu;
+    for (int r = 0; r < 16; ++r) tau[r] = __builtin_inff();
     if (lane < 32) cnt[lane] = 0;
     wave_sync();
     // queries whose list has been written to HBM (each lane re-reads only what it wrote)
@@ -106,13 +113,12 @@ __global__ void __launch_bounds__(256) gt_select(const float* vecs, uint32_t dst
     auto load_tile = [&](uint64_t tile, float4 (&b)[H / 4], float& bnj) __attribute__((always_inline)) {
         const uint64_t j = std::min<uint64_t>(tile + l32, n - 1);
         const float4* row = reinterpret_cast<const float4*>(vecs + j * dstride);
+        // chunks past the row read chunk 0 instead: the query operand is 0 in those
+        // dimensions, so they add nothing, and no load waits on a condition
 #pragma unroll
         for (int c = 0; c < H / 4; ++c) {
             const uint32_t c4 = half * (H / 4) + static_cast<uint32_t>(c);
-            const bool ok = 4u * c4 < dstride;
-            float4 v = row[ok ? c4 : 0u];
-            if (!ok) v = make_float4(0.f, 0.f, 0.f, 0.f);
-            b[c] = v;
+            b[c] = row[4u * c4 < dstride ? c4 : 0u];
         }
         bnj = bn[j];
     };
@@ -139,7 +145,8 @@ __global__ void __launch_bounds__(256) gt_select(const float* vecs, uint32_t dst
                 bsd::beam_merge<2, 1, true>(beam, ck, cm, C, mscr, maux);
                 top[lane] = beam[0];
                 top[64 + lane] = beam[1];
-                const uint32_t nt = static_cast<uint32_t>(readlane64(beam[1], 63) >> 32);
+                const uint64_t last = readlane64(beam[1], 63);
+                const float nt = last == EMPTY_KEY ? __builtin_inff() : bsd::key_dist(last);
                 const uint32_t rr = 4u * (i / 8u) + (i % 4u), hh = (i / 4u) & 1u;
 #pragma unroll
                 for (int r = 0; r < 16; ++r)
@@ -151,23 +158,25 @@ __global__ void __launch_bounds__(256) gt_select(const float* vecs, uint32_t dst
     };
 
     auto step = [&](uint64_t tile, const float4 (&b)[H / 4], float bnj) __attribute__((always_inline)) {
-        f32x16 acc0 = {}, acc1 = {};
+        // one accumulator: a 32x32x2 f32 step occupies the matrix pipe as long as its
+        // result takes, so the dependent chain costs no extra issue slots
+        f32x16 acc = {};
 #pragma unroll
         for (int c = 0; c < H / 4; ++c) {
-            acc0 = __builtin_amdgcn_mfma_f32_32x32x2f32(a[4 * c + 0], b[c].x, acc0, 0, 0, 0);
-            acc1 = __builtin_amdgcn_mfma_f32_32x32x2f32(a[4 * c + 1], b[c].y, acc1, 0, 0, 0);
-            acc0 = __builtin_amdgcn_mfma_f32_32x32x2f32(a[4 * c + 2], b[c].z, acc0, 0, 0, 0);
-            acc1 = __builtin_amdgcn_mfma_f32_32x32x2f32(a[4 * c + 3], b[c].w, acc1, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a[4 * c + 0], b[c].x, acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a[4 * c + 1], b[c].y, acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a[4 * c + 2], b[c].z, acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a[4 * c + 3], b[c].w, acc, 0, 0, 0);
         }
         const uint64_t j = tile + l32;
+        const bool whole = tile + 32 <= r1;  // wave-uniform: only a split's last tile is partial
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-            const float av = bnj - 2.0f * (acc0[r] + acc1[r]);
-            const uint32_t ord = orderable(av);
-            if (j < r1 && ord <= tau[r]) {
+            const float av = __builtin_fmaf(-2.0f, acc[r], bnj);
+            if (av <= tau[r] && (whole || j < r1)) {
                 const uint32_t i = acc_row(r, half);
                 const uint32_t pos = atomicAdd(&cnt[i], 1u);  // < BUF: see compact(32) below
-                buf[i * BUF + pos] = (static_cast<uint64_t>(ord) << 32) | static_cast<uint32_t>(j);
+                buf[i * BUF + pos] = (static_cast<uint64_t>(orderable(av)) << 32) | static_cast<uint32_t>(j);
             }
         }
         wave_sync();
@@ -179,9 +188,11 @@ __global__ void __launch_bounds__(256) gt_select(const float* vecs, uint32_t dst
     load_tile(r0, bA, nA);
     for (uint64_t tile = r0; tile < r1; tile += 64) {
         load_tile(tile + 32, bB, nB);  // rows past the split are loaded (clamped) and ignored
+        __builtin_amdgcn_sched_barrier(0);  // keep the prefetch ahead of this tile's products
         step(tile, bA, nA);
         if (tile + 32 >= r1) break;
         load_tile(tile + 64, bA, nA);
+        __builtin_amdgcn_sched_barrier(0);
         step(tile + 32, bB, nB);
     }
     compact(1);
