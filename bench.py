@@ -339,9 +339,13 @@ def main():
         torch.cuda.synchronize()
         log(f"calibration copy: {args.calib_copy_mib} MiB read + {args.calib_copy_mib} MiB written")
         del x, y
+    t1 = time.time()
     g = search.GPUGraph(base, edges)
+    log(f"index upload (bs_index_create): {time.time() - t1:.2f}s")
     if rq is not None:
+        t1 = time.time()
         g.attach_rabitq(rq[1], rq[2], rq[3])
+        log(f"rabitq records (bs_index_attach_rabitq): {time.time() - t1:.2f}s")
     pdim = rq[3].shape[0] if rq is not None else 0
 
     def cfg_for(mode, topk):
