@@ -406,6 +406,13 @@ def main():
             f"{host.recall(i2, gt)[0]:.4f}, "
             f"E/q {pq2[:, 1].sum() / nq:.1f} D/q {pq2[:, 2].sum() / nq:.1f}, {b2 / kms / 1e6:.0f} GB/s algorithmic")
 
+    # the host-buffer entry point (bs_search): query upload and result download included
+    t1 = time.time()
+    for _ in range(3):
+        g.search(queries, K, args.mode, cfg_for(args.mode, args.topk))
+    host_ms = (time.time() - t1) * 1000.0 / 3
+    log(f"PCIe-inclusive (bs_search, host buffers): {host_ms:.2f} ms/step, {nq / host_ms * 1000:.0f} QPS")
+
     for tk in [int(x) for x in args.sweep.split(",") if x]:
         side_line(args.mode, tk)
     for m in [x for x in args.sweep_modes.split(",") if x]:
