@@ -8,6 +8,9 @@
 //   gen_data     --out-base B.fvecs --out-query Q.fvecs --n N --nq Q --dim D
 //                [--kind mixture|normalized] [--centres 64] [--lo 0] [--hi 128] [--sigma 12]
 //   compute_gt   --base B.fvecs --query Q.fvecs --out GT.ivecs [--k 100]
+//   replicate_queries <input.fvecs|ivecs> <output> <repeats> <fvecs|ivecs>
+//                (positional arguments of src/replicate_queries.cpp:10-24; writes the input
+//                rows `repeats` times in order, for larger query batches)
 #include "bs_host.h"
 
 #include <chrono>
@@ -129,6 +132,34 @@ int main(int argc, char** argv) {
         if (bs_write_vecs(get(a, "--out-base", "base.fvecs").c_str(), 0, b.data(), n, dim) ||
             bs_write_vecs(get(a, "--out-query", "query.fvecs").c_str(), 0, q.data(), nq, dim))
             throw std::runtime_error(bs_host_last_error());
+#elif BS_TOOL == 5
+        if (argc != 5) {
+            std::cerr << "Usage: replicate_queries <input.fvecs|ivecs> <output> <repeats> <format>\n"
+                      << "  format: fvecs | ivecs\n";
+            return 1;
+        }
+        const std::string fmt = argv[4];
+        const long repeats = std::strtol(argv[3], nullptr, 10);
+        if (repeats <= 0) {
+            std::cerr << "repeats must be positive\n";
+            return 1;
+        }
+        if (fmt != "fvecs" && fmt != "ivecs") {
+            std::cerr << "Unknown format: " << fmt << " (use fvecs or ivecs)\n";
+            return 1;
+        }
+        const int is_int = fmt == "ivecs";
+        Buf in;
+        uint64_t n = 0;
+        uint32_t d = 0;
+        if (bs_read_vecs(argv[1], is_int, &in.p, &n, &d)) throw std::runtime_error(bs_host_last_error());
+        // both element types are 4 bytes: tile the raw rows
+        const uint64_t row = static_cast<uint64_t>(d) * 4u, total = n * static_cast<uint64_t>(repeats);
+        std::vector<unsigned char> out(total * row);
+        for (long r = 0; r < repeats; ++r)
+            if (n) std::memcpy(out.data() + static_cast<uint64_t>(r) * n * row, in.p, n * row);
+        if (bs_write_vecs(argv[2], is_int, out.data(), total, d)) throw std::runtime_error(bs_host_last_error());
+        std::cout << n << " x " << repeats << " = " << total << " vectors (dim=" << d << ") -> " << argv[2] << "\n";
 #else
         auto a = args(argc, argv, {});
         Buf b, q;

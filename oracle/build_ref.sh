@@ -12,6 +12,7 @@
 #   cpu_cli          src/cpu_cli.cpp           (reference CPU search CLI, JSON on stdin)
 #   build_graph      src/build_graph.cpp       (Vamana builder, OpenMP)
 #   build_rabitq     src/build_rabitq.cpp      (RaBitQ codebook builder, OpenMP)
+#   replicate_queries src/replicate_queries.cpp (fvecs/ivecs tiler)
 #   ref_fastscan     unittest/test_fastscan.cu:54-145 host functions + oracle/ref_fastscan_main.inc
 set -euo pipefail
 REF="${1:-/root/reference}"
@@ -29,6 +30,7 @@ pids=()
 "$CXX" "${FLAGS[@]}" "$REF/src/cpu_cli.cpp" -o "$OUT/cpu_cli" & pids+=($!)
 "$CXX" "${FLAGS[@]}" -fopenmp "$REF/src/build_graph.cpp" -o "$OUT/build_graph" & pids+=($!)
 "$CXX" "${FLAGS[@]}" -fopenmp "$REF/src/build_rabitq.cpp" -o "$OUT/build_rabitq" & pids+=($!)
+"$CXX" "${FLAGS[@]}" "$REF/src/replicate_queries.cpp" -o "$OUT/replicate_queries" & pids+=($!)
 
 # The fastscan host restatement lives in a CUDA test file; only lines 54-145
 # (cpu_padded_dim .. cpu_estimate) are plain C++.  Check the slice boundaries by

@@ -132,3 +132,36 @@ def test_generators_are_deterministic_and_shaped():
     assert np.allclose(np.linalg.norm(n, axis=1), 1.0, atol=1e-5)
     z = host.gen_mixture(20000, 4, 1, 0.0, 0.0, 1.0, None, 1, 3)  # one centre at 0: N(0,1)
     assert abs(z.mean()) < 0.02 and abs(z.std() - 1.0) < 0.02
+
+
+BIN = os.path.join(os.path.dirname(GOLDEN), os.pardir, "beam_search_collab_amd", "bin")
+
+
+@pytest.mark.skipif(not os.path.exists(os.path.join(BIN, "replicate_queries")), reason="tools not built")
+def test_replicate_queries_tiles_rows():
+    """bin/replicate_queries: same arguments, messages and output as src/replicate_queries.cpp:9-59
+    (rows of the input written `repeats` times in order)"""
+    tool = os.path.join(BIN, "replicate_queries")
+    rng = np.random.default_rng(5)
+    d = tempfile.mkdtemp()
+    q = rng.standard_normal((7, 13)).astype(np.float32)
+    g = rng.integers(-5, 1 << 20, (7, 10)).astype(np.int32)
+    host.write_fvecs(f"{d}/q.fvecs", q)
+    host.write_ivecs(f"{d}/g.ivecs", g)
+    p = subprocess.run([tool, f"{d}/q.fvecs", f"{d}/q3.fvecs", "3", "fvecs"], capture_output=True, text=True)
+    assert p.returncode == 0 and p.stdout == f"7 x 3 = 21 vectors (dim=13) -> {d}/q3.fvecs\n"
+    assert np.array_equal(host.read_fvecs(f"{d}/q3.fvecs"), np.tile(q, (3, 1)))
+    p = subprocess.run([tool, f"{d}/g.ivecs", f"{d}/g4.ivecs", "4", "ivecs"], capture_output=True, text=True)
+    assert p.returncode == 0
+    assert np.array_equal(host.read_ivecs(f"{d}/g4.ivecs"), np.tile(g, (4, 1)))
+    for args, msg in ((["a", "b", "0", "fvecs"], "repeats must be positive"),
+                      ([f"{d}/q.fvecs", f"{d}/x", "2", "bvecs"], "Unknown format"),
+                      (["a", "b"], "Usage: replicate_queries")):
+        p = subprocess.run([tool, *args], capture_output=True, text=True)
+        assert p.returncode == 1 and msg in p.stderr
+    ref = os.path.join(po.REF_DIR, "replicate_queries")
+    if os.path.exists(ref):
+        for src, fmt, r in ((f"{d}/q.fvecs", "fvecs", 5), (f"{d}/g.ivecs", "ivecs", 2)):
+            subprocess.run([ref, src, f"{d}/ref.out", str(r), fmt], check=True, capture_output=True)
+            subprocess.run([tool, src, f"{d}/our.out", str(r), fmt], check=True, capture_output=True)
+            assert sha(f"{d}/ref.out") == sha(f"{d}/our.out")
