@@ -2,10 +2,12 @@
 // Declarations and reference citations: include/bs_hip.h.
 #include "bs_hip.h"
 #include "bs_launch.hpp"
+#include "bs_order.hpp"
 
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <cfloat>
 #include <cstdio>
 #include <cstring>
 #include <string>
@@ -59,7 +61,67 @@ struct bs_index_s {
     float* d_signs = nullptr;
     size_t max_lds = 65536;
     uint32_t cus = 256;  // compute units of the device
+    uint32_t xcds = 1;   // XCDs of the device (workgroup b runs on XCD b mod xcds)
+    // query scheduling (bs_order.hip): pivots, labels, launch map, for up to ORDER_CHUNK
+    // queries per search launch; ws_free orders launches that share the workspace
+    int order_mode = 1;
+    float* d_pivT = nullptr;
+    float* d_pnorm = nullptr;
+    uint32_t* d_ows = nullptr;  // key[ORDER_CHUNK] | qmap[ORDER_CHUNK] | hist[P] | cursor[P]
+    hipEvent_t ws_free = nullptr;
 };
+
+namespace {
+constexpr uint64_t ORDER_CHUNK = 1u << 18;  // queries per ordered search launch
+constexpr uint64_t ORDER_MIN_NQ = 4096;     // mode 1 orders launches of at least this many
+
+// Pivots for query scheduling: ORDER_P rows spread evenly over the index (all rows when
+// n is smaller), re-ordered by a greedy nearest-neighbour tour so that consecutive
+// labels are near in space.  Returns the transposed pivots and their squared norms.
+void make_pivots(const float* vecs, uint64_t n, uint32_t dim, std::vector<float>& pivT, std::vector<float>& pnorm) {
+    const uint32_t P = bso::ORDER_P;
+    const uint32_t m = static_cast<uint32_t>(std::min<uint64_t>(P, n));
+    std::vector<uint64_t> rows(m);
+    for (uint32_t i = 0; i < m; ++i) rows[i] = static_cast<uint64_t>(i) * n / m;
+    std::vector<uint32_t> tour;
+    std::vector<char> used(m, 0);
+    uint32_t cur = 0;
+    used[0] = 1;
+    tour.push_back(0);
+    while (tour.size() < m) {
+        const float* a = vecs + rows[cur] * dim;
+        double best = DBL_MAX;
+        uint32_t bi = 0;
+        for (uint32_t j = 0; j < m; ++j) {
+            if (used[j]) continue;
+            const float* b = vecs + rows[j] * dim;
+            double d = 0;
+            for (uint32_t k = 0; k < dim; ++k) {
+                const double t = static_cast<double>(a[k]) - b[k];
+                d += t * t;
+            }
+            if (d < best) {
+                best = d;
+                bi = j;
+            }
+        }
+        used[bi] = 1;
+        tour.push_back(bi);
+        cur = bi;
+    }
+    pivT.assign(static_cast<size_t>((dim + 1) & ~1u) * P, 0.0f);  // rows for whole k pairs
+    pnorm.assign(P, 1e30f);  // unused slots never win
+    for (uint32_t t = 0; t < m; ++t) {
+        const float* v = vecs + rows[tour[t]] * dim;
+        double nn = 0;
+        for (uint32_t k = 0; k < dim; ++k) {
+            pivT[static_cast<size_t>(k) * P + t] = v[k];
+            nn += static_cast<double>(v[k]) * v[k];
+        }
+        pnorm[t] = static_cast<float>(nn);
+    }
+}
+}  // namespace
 
 extern "C" const char* bs_last_error(void) { return g_err.c_str(); }
 
@@ -102,6 +164,9 @@ extern "C" int bs_index_create(const float* vecs, const uint32_t* edges, uint64_
     int cus = 0;
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, ix->device) == hipSuccess && cus > 0)
         ix->cus = static_cast<uint32_t>(cus);
+    int xcds = 0;
+    if (hipDeviceGetAttribute(&xcds, hipDeviceAttributeNumberOfXccs, ix->device) == hipSuccess && xcds > 0)
+        ix->xcds = std::min<uint32_t>(static_cast<uint32_t>(xcds), bso::ORDER_MAX_X);
     const size_t vbytes = n * ix->dstride * sizeof(float);
     if (hipMalloc(&ix->d_vecs, vbytes) != hipSuccess) {
         delete ix;
@@ -122,6 +187,18 @@ extern "C" int bs_index_create(const float* vecs, const uint32_t* edges, uint64_
                             n, hipMemcpyHostToDevice);
     }
     if (e == hipSuccess) e = hipMemcpy(ix->d_edges, edges, n * degree * sizeof(uint32_t), hipMemcpyHostToDevice);
+    if (e == hipSuccess) {
+        std::vector<float> pivT, pnorm;
+        make_pivots(vecs, n, dim, pivT, pnorm);
+        const size_t ows = (2 * ORDER_CHUNK + 2 * bso::ORDER_P) * sizeof(uint32_t);
+        e = hipMalloc(&ix->d_pivT, pivT.size() * sizeof(float));
+        if (e == hipSuccess) e = hipMalloc(&ix->d_pnorm, pnorm.size() * sizeof(float));
+        if (e == hipSuccess) e = hipMalloc(&ix->d_ows, ows);
+        if (e == hipSuccess) e = hipMemcpy(ix->d_pivT, pivT.data(), pivT.size() * sizeof(float), hipMemcpyHostToDevice);
+        if (e == hipSuccess) e = hipMemcpy(ix->d_pnorm, pnorm.data(), pnorm.size() * sizeof(float), hipMemcpyHostToDevice);
+        if (e == hipSuccess) e = hipMemset(ix->d_ows, 0, ows);
+        if (e == hipSuccess) e = hipEventCreateWithFlags(&ix->ws_free, hipEventDisableTiming);
+    }
     if (e != hipSuccess) {
         bs_index_destroy(ix);
         return fail(BS_EHIP, std::string("upload failed: ") + hipGetErrorString(e));
@@ -200,7 +277,21 @@ extern "C" void bs_index_destroy(bs_index ix) {
     if (ix->d_edges) (void)hipFree(ix->d_edges);
     if (ix->d_recs) (void)hipFree(ix->d_recs);
     if (ix->d_signs) (void)hipFree(ix->d_signs);
+    if (ix->ws_free) {
+        (void)hipEventSynchronize(ix->ws_free);
+        (void)hipEventDestroy(ix->ws_free);
+    }
+    if (ix->d_pivT) (void)hipFree(ix->d_pivT);
+    if (ix->d_pnorm) (void)hipFree(ix->d_pnorm);
+    if (ix->d_ows) (void)hipFree(ix->d_ows);
     delete ix;
+}
+
+extern "C" int bs_index_set_query_order(bs_index ix, int mode) {
+    if (!ix) return fail(BS_EINVAL, "null index");
+    if (mode < 0 || mode > 2) return fail(BS_EINVAL, "query order mode must be 0, 1 or 2");
+    ix->order_mode = mode;
+    return BS_OK;
 }
 
 namespace {
@@ -208,6 +299,7 @@ namespace {
 struct Plan {
     bsd::SearchParams p;
     int TR, CR, PB, mode;
+    uint32_t g;
     dim3 grid, block;
     size_t lds;
 };
@@ -302,7 +394,8 @@ int make_plan(bs_index ix, const bs_search_cfg* cfg, uint64_t nq, Plan& pl) {
         return fail(BS_EINVAL, "LDS per workgroup " + std::to_string(pl.lds) + " B exceeds the device limit " +
                                    std::to_string(ix->max_lds) + " B (lower filter_capacity or queries_per_group)");
     pl.block = dim3(64 * (p.coop > 1 ? p.coop : ny));
-    const uint64_t groups = (nq + ny - 1) / ny;
+    pl.g = p.coop > 1 ? 1u : ny;  // queries per workgroup
+    const uint64_t groups = (nq + pl.g - 1) / pl.g;
     if (groups > 0x7FFFFFFFull) return fail(BS_EINVAL, "too many queries for one launch");
     pl.grid = dim3(static_cast<uint32_t>(groups));
     return BS_OK;
@@ -316,6 +409,51 @@ hipError_t launch(const Plan& pl, hipStream_t s) {
         return bsd::launch_search_rabitq_wide(pl.p, pl.TR, pl.CR, pl.PB, pl.grid, pl.block, pl.lds, s);
     default: return bsd::launch_search_hash(pl.p, pl.TR, pl.CR, pl.PB, pl.grid, pl.block, pl.lds, s);
     }
+}
+
+// The search in launches of at most ORDER_CHUNK queries, each preceded by the query
+// scheduling kernels that fill its launch map.
+hipError_t launch_ordered(bs_index ix, Plan pl, uint64_t nq, hipStream_t s) {
+    const bsd::SearchParams all = pl.p;
+    const uint32_t g = pl.g, X = ix->xcds;
+    hipError_t e = hipStreamWaitEvent(s, ix->ws_free, 0);  // an earlier launch may still read the map
+    for (uint64_t c0 = 0; e == hipSuccess && c0 < nq; c0 += ORDER_CHUNK) {
+        const uint64_t m = std::min(ORDER_CHUNK, nq - c0);
+        bso::OrderParams o;
+        std::memset(&o, 0, sizeof(o));
+        o.queries = all.queries + c0 * all.dim;
+        o.nq = m;
+        o.dim = all.dim;
+        o.pivT = ix->d_pivT;
+        o.pnorm = ix->d_pnorm;
+        o.key = ix->d_ows;
+        o.qmap = ix->d_ows + ORDER_CHUNK;
+        o.hist = o.qmap + ORDER_CHUNK;
+        o.cursor = o.hist + bso::ORDER_P;
+        o.g = g;
+        o.X = X;
+        // XCD x runs workgroups x, x + X, ...; all are full but the launch's last one
+        const uint64_t B = (m + g - 1) / g;
+        uint64_t acc = 0;
+        for (uint32_t x = 0; x < X; ++x) {
+            o.start[x] = static_cast<uint32_t>(acc);
+            uint64_t cnt = (B > x ? (B - 1 - x) / X + 1 : 0) * g;
+            if ((B - 1) % X == x) cnt -= B * g - m;
+            acc += cnt;
+        }
+        e = bso::launch_order(o, s);
+        if (e != hipSuccess) break;
+        pl.p.queries = all.queries + c0 * all.dim;
+        pl.p.results = all.results + c0 * all.K;
+        pl.p.dists = all.dists ? all.dists + c0 * all.K : nullptr;
+        pl.p.per_query = all.per_query ? all.per_query + c0 * 5 : nullptr;
+        pl.p.qmap = o.qmap;
+        pl.p.nq = m;
+        pl.grid = dim3(static_cast<uint32_t>(B));
+        e = launch(pl, s);
+    }
+    if (e == hipSuccess) e = hipEventRecord(ix->ws_free, s);
+    return e;
 }
 
 }  // namespace
@@ -342,7 +480,8 @@ extern "C" int bs_search_device(bs_index ix, const bs_search_cfg* cfg, const flo
         HIP_TRY(hipEventCreate(&e1));
         HIP_TRY(hipEventRecord(e0, s));
     }
-    hipError_t le = launch(pl, s);
+    const bool order = ix->order_mode == 2 || (ix->order_mode == 1 && nq >= ORDER_MIN_NQ);
+    hipError_t le = order ? launch_ordered(ix, pl, nq, s) : launch(pl, s);
     if (le != hipSuccess) {
         if (e0) (void)hipEventDestroy(e0);
         if (e1) (void)hipEventDestroy(e1);

@@ -23,6 +23,7 @@ struct SearchParams {
     uint32_t* results;      // nq * K
     float* dists;           // nq * K or null
     uint32_t* per_query;    // nq * 5 or null: iterations, expansions, dist, est, rerank
+    const uint32_t* qmap;   // nq: launch position -> query, or null (identity)
     uint64_t nq;
     uint32_t dim, dstride, R, K, T;
     uint32_t filter_bits;   // hash: log2 slots; bloom: log2 bits
@@ -44,8 +45,10 @@ __global__ void __launch_bounds__(512) search_kernel(const SearchParams p) {
     const uint32_t lane = lane_id();
     const uint32_t wave = threadIdx.x >> 6;
     const uint32_t coop = p.coop;  // > 1: the workgroup's wavefronts share one query
-    const uint64_t qid = coop > 1 ? static_cast<uint64_t>(blockIdx.x)
+    const uint64_t pos = coop > 1 ? static_cast<uint64_t>(blockIdx.x)
                                   : static_cast<uint64_t>(blockIdx.x) * (blockDim.x >> 6) + wave;
+    if (pos >= p.nq) return;
+    const uint64_t qid = p.qmap ? uniform(p.qmap[pos]) : pos;
     if (qid >= p.nq) return;
 
     char* my = smem + static_cast<size_t>(coop > 1 ? 0u : wave) * p.lds_wave;

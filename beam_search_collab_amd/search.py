@@ -89,6 +89,10 @@ class GPUGraph:
                "bs_index_attach_rabitq")
         self.padded_dim = pdim
 
+    def set_query_order(self, mode: int):
+        """0 off, 1 on for batches of >= 4096 queries (default), 2 always (bs_index_set_query_order)."""
+        _check(_lib.hip().bs_index_set_query_order(self._h, mode), "bs_index_set_query_order")
+
     @property
     def handle(self):
         return self._h

@@ -104,6 +104,18 @@ int bs_search_device(bs_index idx, const bs_search_cfg* cfg, const float* d_quer
                      uint64_t nq, uint32_t* d_results, float* d_dists, uint32_t* d_per_query,
                      void* stream, int sync, bs_stats* stats);
 
+/* Query scheduling (no counterpart in the reference, whose launches run query i in
+ * block i, src/gpu_cli.cu:94-95,111-112,128-129).  Queries are independent, so their order
+ * changes no result; it changes where their gathers hit.  With scheduling on, a search
+ * launch first labels each query with its nearest of 256 pivot rows (fixed at
+ * bs_index_create), sorts the queries by label and gives each XCD a contiguous run of
+ * them, so queries that walk the same region share that XCD's L2.  Results, distances and
+ * per-query counters are written at each query's own row as before.  mode 0: off;
+ * 1 (default): on for calls with nq >= 4096; 2: on for every call.  Scheduled calls run
+ * in launches of at most 262144 queries and share a workspace of the index; a call made
+ * on another stream waits for the previous scheduled call on the device. */
+int bs_index_set_query_order(bs_index idx, int mode);
+
 /* Device pointers of the uploaded index (for tests and profilers). */
 int bs_index_info(bs_index idx, uint64_t* n, uint32_t* dim, uint32_t* degree,
                   uint32_t* padded_dim, int* has_rabitq);

@@ -117,6 +117,31 @@ def test_base_waves_per_query(gpu, nq):
         assert np.array_equal(ids_w, ids_b)
 
 
+@pytest.mark.parametrize("nq", [1, 5, 9, 63, 257, 1000])
+def test_query_order_changes_no_result(gpu, nq):
+    """query scheduling (labels, bucket sort, a run of queries per XCD) only permutes which
+    launch slot runs which query: ids, distances and counters per query are unchanged,
+    including launches with a partial last workgroup and fewer queries than XCDs"""
+    ds = dataset(3000, 64, 32, nq)
+    g = ds["g"]
+    try:
+        for mode in ["base", "warp2", "warp8", "bwarp4", "rabitq"]:
+            fam = mode.rstrip("0123456789")
+            cfg = (GPURabitqSearchCfg(128, 1024, ds["erq"], 1024) if fam == "rabitq"
+                   else GPUBaseSearchCfg(128, 1024, ds["entry"], 1024, 16))
+            out = {}
+            for om in (0, 2):
+                g.set_query_order(om)
+                out[om] = g.search(ds["q"], 10, mode, cfg, with_dists=True)
+            (i0, d0, s0), (i2, d2, s2) = out[0], out[2]
+            assert np.array_equal(i0, i2), (mode, nq)
+            assert d0.tobytes() == d2.tobytes(), (mode, nq)
+            assert {k: v for k, v in s0.items() if k != "kernel_ms"} == {k: v for k, v in s2.items() if k != "kernel_ms"}
+        assert_same(*run_both(ds, "warp4", 10, 64), f"ordered warp4 nq={nq}")
+    finally:
+        g.set_query_order(1)
+
+
 def test_k_equals_topk_and_empty_results(gpu):
     # tiny graph: fewer reachable nodes than K -> trailing 0xFFFFFFFF
     base = host.gen_normalized(40, 16, 3)
@@ -133,6 +158,9 @@ def test_k_equals_topk_and_empty_results(gpu):
 
 
 def test_config_errors(gpu):
+    ds0 = dataset(3000, 64, 32, 5)
+    with pytest.raises(ValueError):
+        ds0["g"].set_query_order(3)
     ds = dataset(3000, 64, 32, 48)
     g = ds["g"]
     with pytest.raises(ValueError):
