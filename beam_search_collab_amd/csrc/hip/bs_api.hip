@@ -109,7 +109,7 @@ void make_pivots(const float* vecs, uint64_t n, uint32_t dim, std::vector<float>
         tour.push_back(bi);
         cur = bi;
     }
-    pivT.assign(static_cast<size_t>((dim + 1) & ~1u) * P, 0.0f);  // rows for whole k pairs
+    pivT.assign(static_cast<size_t>((dim + 15) & ~15u) * P, 0.0f);  // rows for whole blocks of 16
     pnorm.assign(P, 1e30f);  // unused slots never win
     for (uint32_t t = 0; t < m; ++t) {
         const float* v = vecs + rows[tour[t]] * dim;

@@ -39,17 +39,23 @@ __global__ void __launch_bounds__(256) order_key(const OrderParams o) {
     const uint64_t qr = q0 + l32 < o.nq ? q0 + l32 : o.nq - 1;
     const float* qp = o.queries + qr * o.dim;
     const float* pp = o.pivT + 64 * w + l32;
-    const uint32_t dim2 = (o.dim + 1) & ~1u;  // pivT has dim2 rows (an odd dim's last one zero)
+    const uint32_t dim16 = (o.dim + 15) & ~15u;  // pivT has dim16 rows (those past dim zero)
     f32x16 acc0 = {}, acc1 = {};
-#pragma unroll 8
-    for (uint32_t k0 = 0; k0 < dim2; k0 += 2) {
-        const uint32_t k = k0 + half;
-        const float av = qp[k < o.dim ? k : o.dim - 1];  // unconditional load, then select
-        const float a = k < o.dim ? av : 0.0f;
-        const float b0 = pp[static_cast<size_t>(k) * ORDER_P];
-        const float b1 = pp[static_cast<size_t>(k) * ORDER_P + 32];
-        acc0 = __builtin_amdgcn_mfma_f32_32x32x2f32(a, b0, acc0, 0, 0, 0);
-        acc1 = __builtin_amdgcn_mfma_f32_32x32x2f32(a, b1, acc1, 0, 0, 0);
+    for (uint32_t kb = 0; kb < dim16; kb += 16) {
+        float a[8], b0[8], b1[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {  // all loads of 8 k-steps before their products
+            const uint32_t k = kb + 2 * u + half;
+            const float av = qp[k < o.dim ? k : o.dim - 1];  // unconditional load, then select
+            a[u] = k < o.dim ? av : 0.0f;
+            b0[u] = pp[static_cast<size_t>(k) * ORDER_P];
+            b1[u] = pp[static_cast<size_t>(k) * ORDER_P + 32];
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            acc0 = __builtin_amdgcn_mfma_f32_32x32x2f32(a[u], b0[u], acc0, 0, 0, 0);
+            acc1 = __builtin_amdgcn_mfma_f32_32x32x2f32(a[u], b1[u], acc1, 0, 0, 0);
+        }
     }
     const uint32_t p0 = 64 * w + l32, p1 = p0 + 32;
     const float n0 = o.pnorm[p0], n1 = o.pnorm[p1];

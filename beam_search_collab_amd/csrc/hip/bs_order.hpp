@@ -12,7 +12,7 @@ struct OrderParams {
     const float* queries;  // nq * dim
     uint64_t nq;
     uint32_t dim;
-    const float* pivT;     // roundup(dim, 2) * ORDER_P, pivot j's coordinate k at [k * ORDER_P + j]
+    const float* pivT;     // roundup(dim, 16) * ORDER_P, pivot j's coordinate k at [k * ORDER_P + j]
     const float* pnorm;    // ORDER_P squared norms
     uint32_t* key;         // nq labels
     uint32_t* hist;        // ORDER_P counts, zero between launches

@@ -76,7 +76,8 @@ int main() {
         const uint32_t* edges = static_cast<const uint32_t*>(eb.p);
         bs_index ix = nullptr;
         if (bs_index_create(vecs, edges, n, dim, degree, &ix)) return die(bs_last_error());
-        const uint32_t entry = bs_entry_point(vecs, n, dim);
+        uint32_t entry = 0;  // compute_entry_point (src/gpu_cli.cu:55-83), on the device
+        if (bs_index_entry_point(ix, &entry)) return die(bs_last_error());
         std::cout << "data: " << n << " points, dim=" << dim << ", degree=" << degree << ", queries=" << nq
                   << ", entry=" << entry << std::endl;
 

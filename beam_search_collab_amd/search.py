@@ -89,6 +89,12 @@ class GPUGraph:
                "bs_index_attach_rabitq")
         self.padded_dim = pdim
 
+    def entry_point(self) -> int:
+        """compute_entry_point (src/gpu_cli.cu:55-83) on the device: same node as host.entry_point."""
+        e = C.c_uint32(0)
+        _check(_lib.hip().bs_index_entry_point(self._h, C.byref(e)), "bs_index_entry_point")
+        return int(e.value)
+
     def set_query_order(self, mode: int):
         """0 off, 1 on for batches of >= 4096 queries (default), 2 always (bs_index_set_query_order)."""
         _check(_lib.hip().bs_index_set_query_order(self._h, mode), "bs_index_set_query_order")

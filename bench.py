@@ -323,7 +323,6 @@ def main():
         if cache:
             os.makedirs(args.cache, exist_ok=True)
             np.savez(cache, base=base, queries=queries, edges=edges, gt=gt)
-    entry = host.entry_point(base)
     need_rq = args.mode == "rabitq" or "rabitq" in args.sweep_modes
     rq = None
     if need_rq:
@@ -342,6 +341,9 @@ def main():
     t1 = time.time()
     g = search.GPUGraph(base, edges)
     log(f"index upload (bs_index_create): {time.time() - t1:.2f}s")
+    t1 = time.time()
+    entry = g.entry_point()  # compute_entry_point (gpu_cli.cu:55-83) on the device
+    log(f"entry point {entry} on the device (bs_index_entry_point): {time.time() - t1:.3f}s")
     if rq is not None:
         t1 = time.time()
         g.attach_rabitq(rq[1], rq[2], rq[3])

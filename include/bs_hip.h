@@ -116,6 +116,12 @@ int bs_search_device(bs_index idx, const bs_search_cfg* cfg, const float* d_quer
  * on another stream waits for the previous scheduled call on the device. */
 int bs_index_set_query_order(bs_index idx, int mode);
 
+/* The search entry point of the uploaded index, computed on the device: compute_entry_point
+ * (src/gpu_cli.cu:55-83) -- the float centroid accumulated row by row, then the first row of
+ * least float squared distance to it -- with the same float roundings, so *entry equals
+ * bs_entry_point (bs_host.h) on the same vectors.  Synchronous; allocates 4*dim + 8 bytes. */
+int bs_index_entry_point(bs_index idx, uint32_t* entry);
+
 /* Device pointers of the uploaded index (for tests and profilers). */
 int bs_index_info(bs_index idx, uint64_t* n, uint32_t* dim, uint32_t* degree,
                   uint32_t* padded_dim, int* has_rabitq);
