@@ -211,42 +211,38 @@ __device__ __forceinline__ void beam_merge(uint64_t (&beam)[TR], const uint64_t 
 template <int TR, bool RUN>
 __device__ __forceinline__ uint32_t beam_pick(uint64_t (&beam)[TR]) {
     const uint32_t lane = lane_id();
-    uint64_t m[TR];
-#pragma unroll
-    for (int r = 0; r < TR; ++r) m[r] = ballot((static_cast<uint32_t>(beam[r]) & 1u) == 0u);
-    int pr = -1;
+    // first register holding an unexpanded key, and that key's lane: scalar selects over
+    // the registers' ballots (no branches)
+    uint32_t pr = TR;
     uint64_t mp = 0;
 #pragma unroll
     for (int r = TR - 1; r >= 0; --r) {
-        if (m[r] != 0) {
-            pr = r;
-            mp = m[r];
-        }
+        const uint64_t m = ballot((static_cast<uint32_t>(beam[r]) & 1u) == 0u);
+        pr = m != 0 ? static_cast<uint32_t>(r) : pr;
+        mp = m != 0 ? m : mp;
     }
-    if (pr < 0) return INVALID;
+    if (pr == static_cast<uint32_t>(TR)) return INVALID;
     const uint32_t pl = static_cast<uint32_t>(__builtin_ctzll(mp));
-    // (a readlane per candidate register: a select chain over the registers would be
-    // turned into a dynamically indexed array, i.e. scratch memory)
-    uint64_t kp = 0;
+    // the register is chosen by vector selects under a uniform condition, then one
+    // readlane (a readlane per register under a branch costs a branch per register)
+    uint64_t row = beam[0];
 #pragma unroll
-    for (int r = 0; r < TR; ++r)
-        if (r == pr) kp = readlane64(beam[r], pl);
-    int qr = pr;
-    uint32_t ql = pl;
+    for (int r = 1; r < TR; ++r) row = (pr == static_cast<uint32_t>(r)) ? beam[r] : row;
+    const uint64_t kp = readlane64(row, pl);
+    uint32_t qr = pr, ql = pl;
     if constexpr (RUN) {
         // identical keys are rare: look at the next element first, scan only if it repeats
-        uint64_t nxt = EMPTY_KEY;
-        const int nr = pl < 63u ? pr : pr + 1;
-        const uint32_t nl = pl < 63u ? pl + 1u : 0u;
+        const uint32_t nr = pl < 63u ? pr : pr + 1u;
+        uint64_t rown = EMPTY_KEY;
 #pragma unroll
-        for (int r = 0; r < TR; ++r)
-            if (r == nr) nxt = readlane64(beam[r], nl);
+        for (int r = 0; r < TR; ++r) rown = (nr == static_cast<uint32_t>(r)) ? beam[r] : rown;
+        const uint64_t nxt = readlane64(rown, (pl + 1u) & 63u);
         if (nxt == kp) {
 #pragma unroll
             for (int r = 0; r < TR; ++r) {
                 const uint64_t mm = ballot(beam[r] == kp);
-                if (r >= pr && mm != 0) {
-                    qr = r;
+                if (static_cast<uint32_t>(r) >= pr && mm != 0) {
+                    qr = static_cast<uint32_t>(r);
                     ql = 63u - static_cast<uint32_t>(__builtin_clzll(mm));
                 }
             }
@@ -256,10 +252,8 @@ __device__ __forceinline__ uint32_t beam_pick(uint64_t (&beam)[TR]) {
     const uint32_t bit = (lane == ql) ? 1u : 0u;
 #pragma unroll
     for (int r = 0; r < TR; ++r) {
-        if (r == qr) {
-            const uint32_t lo = static_cast<uint32_t>(beam[r]) | bit;
-            beam[r] = (beam[r] & 0xFFFFFFFF00000000ull) | lo;
-        }
+        const uint32_t lo = static_cast<uint32_t>(beam[r]) | ((qr == static_cast<uint32_t>(r)) ? bit : 0u);
+        beam[r] = (beam[r] & 0xFFFFFFFF00000000ull) | lo;
     }
     return key_id(kp);
 }
