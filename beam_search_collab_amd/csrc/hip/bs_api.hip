@@ -127,8 +127,14 @@ extern "C" const char* bs_last_error(void) { return g_err.c_str(); }
 
 // helpers for the primitive entry points (bs_debug.hip)
 int bs_internal_vecs(bs_index ix, const float** vecs, uint32_t* dstride) {
+    if (!ix) return fail(BS_EINVAL, "null index");
     *vecs = ix->d_vecs;
     *dstride = ix->dstride;
+    return BS_OK;
+}
+int bs_internal_edges(bs_index ix, const uint32_t** edges) {
+    if (!ix) return fail(BS_EINVAL, "null index");
+    *edges = ix->d_edges;
     return BS_OK;
 }
 void bs_internal_set_error(const std::string& msg) { g_err = msg; }
@@ -207,6 +213,31 @@ extern "C" int bs_index_create(const float* vecs, const uint32_t* edges, uint64_
     return BS_OK;
 }
 
+// Node records [vec dstride | ids R | tx R | fdq R | fvq R | codes R*cws | 0...] (rw words),
+// a thread per word.  vecs/edges/factors/codes/recs point at the chunk's first node.
+__global__ void __launch_bounds__(256) assemble_records(const float* vecs, const uint32_t* edges,
+                                                        const float* factors, const uint32_t* codes, uint64_t m,
+                                                        uint32_t dstride, uint32_t R, uint32_t wpp, uint32_t cws,
+                                                        uint32_t rw, uint32_t* recs) {
+    const uint64_t t = static_cast<uint64_t>(blockIdx.x) * 256 + threadIdx.x;
+    if (t >= m * rw) return;
+    const uint64_t u = t / rw;
+    const uint32_t w = static_cast<uint32_t>(t - u * rw);
+    const uint32_t ids = dstride, fac = ids + R, cod = fac + 3 * R;
+    uint32_t v = 0;
+    if (w < ids) {
+        v = __float_as_uint(vecs[u * dstride + w]);
+    } else if (w < fac) {
+        v = edges[u * R + (w - ids)];
+    } else if (w < cod) {
+        v = __float_as_uint(factors[u * 3 * R + (w - fac)]);
+    } else if (w - cod < R * cws) {
+        const uint32_t j = (w - cod) / cws, k = (w - cod) % cws;
+        v = k < wpp ? codes[(u * R + j) * wpp + k] : 0u;
+    }
+    recs[t] = v;
+}
+
 extern "C" int bs_index_attach_rabitq(bs_index ix, const uint32_t* codes, const float* factors,
                                       const float* signs, uint32_t padded_dim) {
     if (!ix || !codes || !factors || !signs) return fail(BS_EINVAL, "null argument");
@@ -218,7 +249,6 @@ extern "C" int bs_index_attach_rabitq(bs_index ix, const uint32_t* codes, const 
     const uint32_t cws = bsd::quad_shape(wpp, R).cws;  // code words per neighbour, >= 4
     uint32_t rw = ix->dstride + R + 3 * R + R * cws;
     rw = (rw + 31) & ~31u;
-    // assemble the records on the host in blocks and upload
     if (ix->d_recs) {
         (void)hipFree(ix->d_recs);
         ix->d_recs = nullptr;
@@ -237,26 +267,32 @@ extern "C" int bs_index_attach_rabitq(bs_index ix, const uint32_t* codes, const 
     ix->rec_ids = ix->dstride;
     ix->rec_fac = ix->rec_ids + R;
     ix->rec_codes = ix->rec_fac + 3 * R;
-    const uint64_t block = std::max<uint64_t>(1, (64ull << 20) / (4ull * rw));
-    std::vector<uint32_t> host(block * rw);
-    std::vector<float> vtmp(block * ix->dstride);
-    std::vector<uint32_t> etmp(block * R);
-    for (uint64_t r0 = 0; r0 < ix->n; r0 += block) {
-        const uint64_t m = std::min(block, ix->n - r0);
-        HIP_TRY(hipMemcpy(vtmp.data(), ix->d_vecs + r0 * ix->dstride, m * ix->dstride * 4, hipMemcpyDeviceToHost));
-        HIP_TRY(hipMemcpy(etmp.data(), ix->d_edges + r0 * R, m * R * 4, hipMemcpyDeviceToHost));
-        std::fill(host.begin(), host.begin() + m * rw, 0u);
-        for (uint64_t i = 0; i < m; ++i) {
-            uint32_t* rec = host.data() + i * rw;
-            std::memcpy(rec, vtmp.data() + i * ix->dstride, 4ull * ix->dstride);
-            std::memcpy(rec + ix->rec_ids, etmp.data() + i * R, 4ull * R);
-            std::memcpy(rec + ix->rec_fac, factors + (r0 + i) * 3 * R, 12ull * R);
-            const uint32_t* src = codes + (r0 + i) * R * wpp;
-            for (uint32_t j = 0; j < R; ++j)
-                std::memcpy(rec + ix->rec_codes + j * cws, src + j * wpp, 4ull * wpp);
-        }
-        HIP_TRY(hipMemcpy(ix->d_recs + r0 * rw, host.data(), m * rw * 4ull, hipMemcpyHostToDevice));
+    // upload codes and factors in chunks of nodes; a kernel writes the chunk's records from
+    // them and the resident vectors and edges
+    const uint64_t chunk = std::max<uint64_t>(1, (256ull << 20) / (4ull * R * (wpp + 3)));
+    const uint64_t m0 = std::min(chunk, ix->n);
+    uint32_t* d_codes = nullptr;
+    float* d_fac = nullptr;
+    if (hipMalloc(&d_codes, m0 * R * wpp * 4ull) != hipSuccess || hipMalloc(&d_fac, m0 * 3ull * R * 4ull) != hipSuccess) {
+        if (d_codes) (void)hipFree(d_codes);
+        return fail(BS_ENOMEM, "hipMalloc of the record staging buffers failed");
     }
+    hipError_t e = hipSuccess;
+    for (uint64_t r0 = 0; e == hipSuccess && r0 < ix->n; r0 += chunk) {
+        const uint64_t m = std::min(chunk, ix->n - r0);
+        e = hipMemcpy(d_codes, codes + r0 * R * wpp, m * R * wpp * 4ull, hipMemcpyHostToDevice);
+        if (e == hipSuccess) e = hipMemcpy(d_fac, factors + r0 * 3ull * R, m * 3ull * R * 4ull, hipMemcpyHostToDevice);
+        if (e != hipSuccess) break;
+        const uint64_t words = m * rw;
+        hipLaunchKernelGGL(assemble_records, dim3(static_cast<uint32_t>((words + 255) / 256)), dim3(256), 0, nullptr,
+                           ix->d_vecs + r0 * ix->dstride, ix->d_edges + r0 * R, d_fac, d_codes, m, ix->dstride, R, wpp,
+                           cws, rw, ix->d_recs + r0 * rw);
+        e = hipGetLastError();
+    }
+    if (e == hipSuccess) e = hipDeviceSynchronize();
+    (void)hipFree(d_codes);
+    (void)hipFree(d_fac);
+    if (e != hipSuccess) return fail(BS_EHIP, std::string("rabitq record assembly: ") + hipGetErrorString(e));
     return BS_OK;
 }
 

@@ -1,20 +1,31 @@
-// Index preparation on the device: the search entry point.
+// Index preparation on the device: the search entry point and the RaBitQ codebook.
 //
 // compute_entry_point (src/gpu_cli.cu:55-83): a float centroid accumulated row after row
 // (centroid[d] += row[d] * inv, inv = 1 / n), then the first row of least float squared
 // distance to it (diff = row[d] - centroid[d]; dist += diff * diff, dimensions in order;
 // a row replaces the best only if dist < best, starting from FLT_MAX and row 0).  The
 // float roundings of both loops are reproduced exactly, so the node is the reference's.
+//
+// build_rabitq (src/build_rabitq.cpp:59-99,138-264): the same two steps in double for the
+// codebook's medoid, every node's rotation WHT(signs * [v, 0...]) once, then a thread per
+// edge for the residual, its 1-bit code and the float parts of its factors, in the
+// reference's operation order; the three factor products, which the reference forms in
+// long double, are finished on the host.
 #include "bs_hip.h"
 #include "wave.hpp"
 
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cfloat>
 #include <cstring>
+#include <random>
 #include <string>
+#include <thread>
+#include <vector>
 
 int bs_internal_vecs(bs_index idx, const float** vecs, uint32_t* dstride);
+int bs_internal_edges(bs_index idx, const uint32_t** edges);
 void bs_internal_set_error(const std::string& msg);
 
 namespace bsp {
@@ -33,15 +44,21 @@ __device__ __forceinline__ uint32_t orderable(float f) {
 // parallelism is across dimensions: workgroup x owns dimensions [64x, 64x + 64), its
 // first wavefront adds (lane = dimension) while the other 15 wavefronts stream the next
 // chunk of rows into the other half of a double buffer in LDS.
+//   float:  c += row[d] * inv                       (compute_entry_point)
+//   double: c += (double)row[d], then c / n         (find_medoid)
+template <typename T>
 __global__ void __launch_bounds__(EP_THREADS) entry_centroid(const float* vecs, uint64_t n, uint32_t dim,
-                                                            uint32_t dstride, float inv, float* cent,
+                                                            uint32_t dstride, float inv, T* cent,
                                                             unsigned long long* best) {
     extern __shared__ float buf[];  // [2][EP_ROWS][64]
     const uint32_t lane = lane_id(), wave = uniform(threadIdx.x >> 6);
     const uint32_t col0 = blockIdx.x * 64;
     const uint64_t nchunk = (n + EP_ROWS - 1) / EP_ROWS;
-    if (blockIdx.x == 0 && threadIdx.x == 0)
-        *best = static_cast<unsigned long long>(orderable(FLT_MAX)) << 32;  // (FLT_MAX, row 0)
+    if (blockIdx.x == 0 && threadIdx.x == 0) {
+        // float: the key (FLT_MAX, row 0); double: the distance bits of DBL_MAX
+        if constexpr (sizeof(T) == 4) *best = static_cast<unsigned long long>(orderable(FLT_MAX)) << 32;
+        else *best = static_cast<unsigned long long>(__double_as_longlong(DBL_MAX));
+    }
     // stage chunk c into buffer half h with threads [t0, EP_THREADS)
     auto stage = [&](uint64_t c, uint32_t h, uint32_t t0) __attribute__((always_inline)) {
         float* dst = buf + h * (EP_ROWS * 64);
@@ -56,19 +73,25 @@ __global__ void __launch_bounds__(EP_THREADS) entry_centroid(const float* vecs, 
     };
     stage(0, 0, 0);
     __syncthreads();
-    float s = 0.0f;
+    T s = 0;
     for (uint64_t c = 0; c < nchunk; ++c) {
         const uint32_t h = static_cast<uint32_t>(c & 1);
         if (wave == 0) {
             const float* src = buf + h * (EP_ROWS * 64) + lane;
             const uint32_t rows = static_cast<uint32_t>(n - c * EP_ROWS < EP_ROWS ? n - c * EP_ROWS : EP_ROWS);
+            if constexpr (sizeof(T) == 4) {
 #pragma unroll 16
-            for (uint32_t r = 0; r < rows; ++r) s = s + src[r * 64] * inv;
+                for (uint32_t r = 0; r < rows; ++r) s = s + src[r * 64] * inv;
+            } else {
+#pragma unroll 16
+                for (uint32_t r = 0; r < rows; ++r) s = s + static_cast<double>(src[r * 64]);
+            }
         } else if (c + 1 < nchunk) {
             stage(c + 1, h ^ 1u, 64);
         }
         __syncthreads();
     }
+    if constexpr (sizeof(T) == 8) s = s / static_cast<double>(n);
     if (wave == 0 && col0 + lane < dim) cent[col0 + lane] = s;
 }
 
@@ -113,6 +136,118 @@ __global__ void __launch_bounds__(256) entry_nearest(const float* vecs, uint64_t
     if (lane_id() == 0 && key != ~0ull) atomicMin(best, key);
 }
 
+// find_medoid's nearest row in double: pass 1 stores every row's distance and the least
+// distance bits (non-negative doubles order as their bit patterns), pass 2 the least row
+// index at that distance.
+__global__ void __launch_bounds__(256) medoid_dist(const float* vecs, uint64_t n, uint32_t dim, uint32_t dstride,
+                                                   const double* cent, double* dist, unsigned long long* best) {
+    __shared__ double c[1024];
+    for (uint32_t k = threadIdx.x; k < dim; k += 256) c[k] = cent[k];
+    __syncthreads();
+    const uint64_t i = static_cast<uint64_t>(blockIdx.x) * 256 + threadIdx.x;
+    unsigned long long key = ~0ull;
+    if (i < n) {
+        const float* row = vecs + i * dstride;
+        double s = 0.0;
+        for (uint32_t k = 0; k < dim; ++k) {
+            const double d = static_cast<double>(row[k]) - c[k];
+            s = s + d * d;
+        }
+        dist[i] = s;
+        if (s < DBL_MAX) key = static_cast<unsigned long long>(__double_as_longlong(s));
+    }
+    unsigned long long t;
+    t = xor_lane64<1>(key); key = t < key ? t : key;
+    t = xor_lane64<2>(key); key = t < key ? t : key;
+    t = xor_lane64<4>(key); key = t < key ? t : key;
+    t = xor_lane64<8>(key); key = t < key ? t : key;
+    t = xor_lane64<16>(key); key = t < key ? t : key;
+    t = xor_lane64<32>(key); key = t < key ? t : key;
+    if (lane_id() == 0 && key != ~0ull) atomicMin(best, key);
+}
+
+__global__ void __launch_bounds__(256) medoid_index(uint64_t n, const double* dist, const unsigned long long* best,
+                                                    uint32_t* index) {
+    const uint64_t i = static_cast<uint64_t>(blockIdx.x) * 256 + threadIdx.x;
+    const unsigned long long b = *best;  // still DBL_MAX: no row qualified
+    if (i < n && b != static_cast<unsigned long long>(__double_as_longlong(DBL_MAX)) &&
+        static_cast<unsigned long long>(__double_as_longlong(dist[i])) == b)
+        atomicMin(index, static_cast<uint32_t>(i));
+}
+
+// rotate_vector (build_rabitq.cpp:19-55): r = WHT(signs * [v, 0...]), one wavefront per
+// node in LDS.  Stage len pairs (a, a + len) for a with bit len clear; the pairs of a
+// stage are disjoint, so any lane order gives the sequential loop's values.
+__global__ void __launch_bounds__(256) rq_rotate(const float* vecs, uint32_t dstride, uint64_t n, uint32_t dim,
+                                                 uint32_t pdim, const float* signs, float* rot) {
+    extern __shared__ float sh[];
+    const uint32_t lane = lane_id(), w = uniform(threadIdx.x >> 6);
+    const uint64_t u = static_cast<uint64_t>(blockIdx.x) * 4 + w;
+    if (u >= n) return;
+    float* x = sh + w * pdim;
+    for (uint32_t d = lane; d < pdim; d += 64) x[d] = d < dim ? vecs[u * dstride + d] * signs[d] : 0.0f;
+    wave_sync();
+    for (uint32_t len = 1; len < pdim; len <<= 1) {
+        for (uint32_t t = lane; t < pdim / 2; t += 64) {
+            const uint32_t a = (t / len) * 2 * len + (t % len), b = a + len;
+            const float xa = x[a], xb = x[b];
+            x[a] = xa + xb;
+            x[b] = xa - xb;
+        }
+        wave_sync();
+    }
+    for (uint32_t d = lane; d < pdim; d += 64) rot[u * pdim + d] = x[d];
+}
+
+// Thread per edge (build_rabitq.cpp:217-256): residual = v_rot - u_rot over the first
+// dim components; sqr_r, the code bits, bin_sum, fac_x0 and fac_x1 accumulate in
+// dimension order as in the reference's loops.  out: (r_norm, fac_x0 / r_norm,
+// fac_x1 * fac_norm, bin_sum); an absent neighbour gets bin_sum = -1.
+__global__ void __launch_bounds__(256) rq_edges(const float* rot, const uint32_t* edges, uint64_t ne, uint32_t R,
+                                                uint32_t dim, uint32_t pdim, uint32_t wpp, float fac_norm,
+                                                uint32_t* codes, float4* out) {
+    const uint64_t e = static_cast<uint64_t>(blockIdx.x) * 256 + threadIdx.x;
+    if (e >= ne) return;
+    const uint32_t v = edges[e];
+    uint32_t* cw = codes + e * wpp;
+    if (v == 0xFFFFFFFFu) {
+        for (uint32_t w = 0; w < wpp; ++w) cw[w] = 0u;
+        out[e] = make_float4(0.0f, 0.0f, 0.0f, __int_as_float(-1));
+        return;
+    }
+    const float4* ur = reinterpret_cast<const float4*>(rot + (e / R) * pdim);
+    const float4* vr = reinterpret_cast<const float4*>(rot + static_cast<uint64_t>(v) * pdim);
+    float sqr = 0.0f, fx0 = 0.0f, fx1 = 0.0f;
+    int bin_sum = 0;
+    uint32_t word = 0;
+    for (uint32_t d4 = 0; d4 * 4 < dim; ++d4) {
+        const float4 a = vr[d4], b = ur[d4];
+        const float av[4] = {a.x, a.y, a.z, a.w}, bv[4] = {b.x, b.y, b.z, b.w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const uint32_t d = d4 * 4 + j;
+            if (d < dim) {
+                const float res = av[j] - bv[j];
+                sqr = sqr + res * res;
+                const bool pos = res > 0.0f;
+                word |= pos ? (1u << (d & 31u)) : 0u;
+                bin_sum += pos ? 1 : 0;
+                const float sv = pos ? 1.0f : -1.0f;
+                fx0 = fx0 + res * sv * fac_norm;
+                fx1 = fx1 + bv[j] * sv;
+            }
+            if (d < dim && (d & 31u) == 31u) {
+                cw[d >> 5] = word;
+                word = 0;
+            }
+        }
+    }
+    for (uint32_t w = (dim + 31) / 32; w < wpp; ++w) cw[w] = 0u;
+    if (dim & 31u) cw[dim >> 5] = word;
+    const float r_norm = sqrtf(sqr) + 1e-10f;
+    out[e] = make_float4(r_norm, fx0 / r_norm, fx1 * fac_norm, __int_as_float(bin_sum));
+}
+
 }  // namespace bsp
 
 namespace {
@@ -140,10 +275,10 @@ extern "C" int bs_index_entry_point(bs_index idx, uint32_t* entry) {
     }
     const float inv = 1.0f / static_cast<float>(n);
     const size_t lds = 2 * bsp::EP_ROWS * 64 * sizeof(float);
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(bsp::entry_centroid),
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(bsp::entry_centroid<float>),
                                        hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
     if (e == hipSuccess) {
-        hipLaunchKernelGGL(bsp::entry_centroid, dim3((dim + 63) / 64), dim3(bsp::EP_THREADS), lds, nullptr, vecs, n,
+        hipLaunchKernelGGL(bsp::entry_centroid<float>, dim3((dim + 63) / 64), dim3(bsp::EP_THREADS), lds, nullptr, vecs, n,
                            dim, dstride, inv, cent, best);
         e = hipGetLastError();
     }
@@ -158,5 +293,132 @@ extern "C" int bs_index_entry_point(bs_index idx, uint32_t* entry) {
     (void)hipFree(best);
     if (e != hipSuccess) return pfail(BS_EHIP, std::string("entry point: ") + hipGetErrorString(e));
     *entry = static_cast<uint32_t>(key & 0xFFFFFFFFull);
+    return BS_OK;
+}
+
+extern "C" int bs_index_build_rabitq(bs_index idx, uint32_t seed, uint32_t* codes_out, float* factors_out,
+                                     float* signs_out, uint32_t* entry_out) {
+    if (!codes_out || !factors_out || !signs_out || !entry_out) return pfail(BS_EINVAL, "null output");
+    const float* vecs = nullptr;
+    const uint32_t* edges = nullptr;
+    uint32_t dstride = 0;
+    int rc = bs_internal_vecs(idx, &vecs, &dstride);
+    if (rc) return rc;
+    rc = bs_internal_edges(idx, &edges);
+    if (rc) return rc;
+    uint64_t n = 0;
+    uint32_t dim = 0, R = 0;
+    rc = bs_index_info(idx, &n, &dim, &R, nullptr, nullptr);
+    if (rc) return rc;
+    uint32_t pdim = 1;
+    while (pdim < dim) pdim <<= 1;
+    if (pdim < 32) return pfail(BS_EINVAL, "rabitq needs a padded dim >= 32 (dim > 16)");
+    const uint32_t wpp = pdim / 32;
+    const uint64_t ne = n * R;
+
+    // signs (build_rabitq.cpp:138-145): mt19937_64(seed), a fair coin per padded dimension
+    {
+        std::mt19937_64 gen(seed);
+        std::uniform_int_distribution<int> coin(0, 1);
+        const float scale = 1.0f / std::sqrt(static_cast<float>(pdim));
+        for (uint32_t i = 0; i < pdim; ++i) signs_out[i] = static_cast<float>(2 * coin(gen) - 1) * scale;
+    }
+    const float fac_norm = 1.0f / std::sqrt(static_cast<float>(dim));
+
+    float* d_signs = nullptr;
+    float* d_rot = nullptr;
+    uint32_t* d_codes = nullptr;
+    float4* d_out = nullptr;
+    double* d_cent = nullptr;
+    double* d_dist = nullptr;
+    unsigned long long* d_best = nullptr;
+    uint32_t* d_index = nullptr;
+    auto release = [&]() {
+        if (d_signs) (void)hipFree(d_signs);
+        if (d_rot) (void)hipFree(d_rot);
+        if (d_codes) (void)hipFree(d_codes);
+        if (d_out) (void)hipFree(d_out);
+        if (d_cent) (void)hipFree(d_cent);
+        if (d_dist) (void)hipFree(d_dist);
+        if (d_best) (void)hipFree(d_best);
+        if (d_index) (void)hipFree(d_index);
+    };
+    if (hipMalloc(&d_signs, pdim * sizeof(float)) != hipSuccess || hipMalloc(&d_rot, n * pdim * sizeof(float)) != hipSuccess ||
+        hipMalloc(&d_codes, ne * wpp * sizeof(uint32_t)) != hipSuccess || hipMalloc(&d_out, ne * sizeof(float4)) != hipSuccess ||
+        hipMalloc(&d_cent, dim * sizeof(double)) != hipSuccess || hipMalloc(&d_dist, n * sizeof(double)) != hipSuccess ||
+        hipMalloc(&d_best, sizeof(unsigned long long)) != hipSuccess || hipMalloc(&d_index, sizeof(uint32_t)) != hipSuccess) {
+        release();
+        return pfail(BS_ENOMEM, "hipMalloc of the codebook work buffers failed");
+    }
+    std::vector<float4> st(ne);
+    const uint32_t init_index = 0xFFFFFFFFu;
+    hipError_t e = hipMemcpy(d_signs, signs_out, pdim * sizeof(float), hipMemcpyHostToDevice);
+    if (e == hipSuccess) e = hipMemcpy(d_index, &init_index, sizeof(init_index), hipMemcpyHostToDevice);
+    // medoid (find_medoid, build_rabitq.cpp:59-99) in double
+    const size_t lds = 2 * bsp::EP_ROWS * 64 * sizeof(float);
+    if (e == hipSuccess)
+        e = hipFuncSetAttribute(reinterpret_cast<const void*>(bsp::entry_centroid<double>),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
+    if (e == hipSuccess) {
+        hipLaunchKernelGGL(bsp::entry_centroid<double>, dim3((dim + 63) / 64), dim3(bsp::EP_THREADS), lds, nullptr,
+                           vecs, n, dim, dstride, 0.0f, d_cent, d_best);
+        e = hipGetLastError();
+    }
+    const dim3 rows_grid(static_cast<uint32_t>((n + 255) / 256));
+    if (e == hipSuccess) {
+        hipLaunchKernelGGL(bsp::medoid_dist, rows_grid, dim3(256), 0, nullptr, vecs, n, dim, dstride, d_cent, d_dist,
+                           d_best);
+        e = hipGetLastError();
+    }
+    if (e == hipSuccess) {
+        hipLaunchKernelGGL(bsp::medoid_index, rows_grid, dim3(256), 0, nullptr, n, d_dist, d_best, d_index);
+        e = hipGetLastError();
+    }
+    // rotations, then the edges
+    if (e == hipSuccess) {
+        hipLaunchKernelGGL(bsp::rq_rotate, dim3(static_cast<uint32_t>((n + 3) / 4)), dim3(256),
+                           4 * pdim * sizeof(float), nullptr, vecs, dstride, n, dim, pdim, d_signs, d_rot);
+        e = hipGetLastError();
+    }
+    if (e == hipSuccess) {
+        hipLaunchKernelGGL(bsp::rq_edges, dim3(static_cast<uint32_t>((ne + 255) / 256)), dim3(256), 0, nullptr, d_rot,
+                           edges, ne, R, dim, pdim, wpp, fac_norm, d_codes, d_out);
+        e = hipGetLastError();
+    }
+    uint32_t medoid = 0;
+    if (e == hipSuccess) e = hipMemcpy(&medoid, d_index, sizeof(medoid), hipMemcpyDeviceToHost);
+    if (e == hipSuccess) e = hipMemcpy(codes_out, d_codes, ne * wpp * sizeof(uint32_t), hipMemcpyDeviceToHost);
+    if (e == hipSuccess) e = hipMemcpy(st.data(), d_out, ne * sizeof(float4), hipMemcpyDeviceToHost);
+    release();
+    if (e != hipSuccess) return pfail(BS_EHIP, std::string("rabitq codebook: ") + hipGetErrorString(e));
+    *entry_out = medoid == 0xFFFFFFFFu ? 0u : medoid;  // no row below DBL_MAX: row 0, as the reference
+
+    // the factor products in long double (build_rabitq.cpp:250-256), on the host threads
+    auto finish = [&](uint64_t u0, uint64_t u1) {
+        for (uint64_t u = u0; u < u1; ++u) {
+            float* tx = factors_out + u * 3 * R;
+            float* dq = tx + R;
+            float* vq = dq + R;
+            for (uint32_t i = 0; i < R; ++i) {
+                const float4 t = st[u * R + i];
+                const int bin_sum = __builtin_bit_cast(int, t.w);
+                if (bin_sum < 0) {
+                    tx[i] = FLT_MAX;
+                    dq[i] = 0.0f;
+                    vq[i] = 0.0f;
+                    continue;
+                }
+                const float r_norm = t.x, fx0 = t.y, fx1 = t.z;
+                const long double x_x0 = static_cast<long double>(r_norm) / fx0;
+                tx[i] = static_cast<float>(static_cast<long double>(r_norm) * r_norm + 2.0L * x_x0 * fx1);
+                dq[i] = static_cast<float>(-2.0L * x_x0 * fac_norm);
+                vq[i] = dq[i] * static_cast<float>(2 * bin_sum - static_cast<int>(dim));
+            }
+        }
+    };
+    const uint32_t T = std::max(1u, std::min(32u, std::thread::hardware_concurrency()));
+    std::vector<std::thread> pool;
+    for (uint32_t t = 0; t < T; ++t) pool.emplace_back(finish, n * t / T, n * (t + 1) / T);
+    for (auto& th : pool) th.join();
     return BS_OK;
 }

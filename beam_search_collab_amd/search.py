@@ -95,6 +95,21 @@ class GPUGraph:
         _check(_lib.hip().bs_index_entry_point(self._h, C.byref(e)), "bs_index_entry_point")
         return int(e.value)
 
+    def build_rabitq(self, seed: int = 12345):
+        """build_rabitq (src/build_rabitq.cpp) on the device from the uploaded graph:
+        (entry, codes, factors, signs), byte-identical to host.build_rabitq."""
+        pdim = 1
+        while pdim < self.dim:
+            pdim <<= 1
+        wpp = pdim // 32
+        codes = np.empty((self.n, self.degree * wpp), dtype=np.uint32)
+        factors = np.empty((self.n, 3 * self.degree), dtype=np.float32)
+        signs = np.empty(pdim, dtype=np.float32)
+        e = C.c_uint32(0)
+        _check(_lib.hip().bs_index_build_rabitq(self._h, seed, _ptr(codes), _ptr(factors), _ptr(signs), C.byref(e)),
+               "bs_index_build_rabitq")
+        return int(e.value), codes, factors, signs
+
     def set_query_order(self, mode: int):
         """0 off, 1 on for batches of >= 4096 queries (default), 2 always (bs_index_set_query_order)."""
         _check(_lib.hip().bs_index_set_query_order(self._h, mode), "bs_index_set_query_order")

@@ -122,6 +122,17 @@ int bs_index_set_query_order(bs_index idx, int mode);
  * bs_entry_point (bs_host.h) on the same vectors.  Synchronous; allocates 4*dim + 8 bytes. */
 int bs_index_entry_point(bs_index idx, uint32_t* entry);
 
+/* The RaBitQ codebook of the uploaded index, computed on the device: build_rabitq
+ * (src/build_rabitq.cpp:59-99,138-264) -- sign table from mt19937_64(seed), per edge the
+ * residual of the rotated vectors, its 1-bit code and the factors (tx | fdq | fvq), entry =
+ * medoid with a double centroid -- byte-identical to bs_build_rabitq (bs_host.h).  Host
+ * outputs: codes n*degree*(pdim/32) u32, factors n*3*degree f32, signs pdim f32, entry.
+ * The float work runs on the device; the factor products the reference forms in long
+ * double are finished on the host.  Synchronous; allocates work buffers (rotations
+ * n*pdim f32, codes, 16 B per edge).  dim > 16. */
+int bs_index_build_rabitq(bs_index idx, uint32_t seed, uint32_t* codes, float* factors, float* signs,
+                          uint32_t* entry);
+
 /* Device pointers of the uploaded index (for tests and profilers). */
 int bs_index_info(bs_index idx, uint64_t* n, uint32_t* dim, uint32_t* degree,
                   uint32_t* padded_dim, int* has_rabitq);

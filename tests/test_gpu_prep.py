@@ -48,3 +48,60 @@ def test_entry_point_ties_and_non_finite_rows(gpu):
     base3[::7, 3] = np.inf
     base3[5, 0] = np.nan
     assert gpu_entry(base3) == host.entry_point(base3)
+
+
+def _graph(n, dim, degree, seed, kind="mixture"):
+    if kind == "mixture":
+        base = host.gen_mixture(n, dim, 8, 0.0, 128.0, 12.0, 0.0, seed, seed + 1)
+    else:
+        base = host.gen_normalized(n, dim, seed)
+    edges = host.build_vamana(base, degree, 2 * degree, 1.2, 7, exact=False, threads=0)
+    return base, edges
+
+
+@pytest.mark.parametrize("n,dim,degree,kind", [(3000, 17, 8, "mixture"), (3000, 30, 16, "normalized"),
+                                               (5000, 100, 32, "normalized"), (5000, 128, 32, "mixture"),
+                                               (2000, 200, 24, "mixture"), (1500, 960, 32, "mixture"),
+                                               (1000, 1024, 12, "normalized")])
+def test_device_rabitq_codebook_is_byte_identical(gpu, n, dim, degree, kind):
+    """bs_index_build_rabitq equals the host builder (itself byte-identical to the reference
+    build_rabitq) in every code word, factor bit, sign and the medoid, with absent edges"""
+    base, edges = _graph(n, dim, degree, dim + degree, kind)
+    edges[::5, -1] = 0xFFFFFFFF
+    edges[7, :] = 0xFFFFFFFF
+    g = search.GPUGraph(base, edges)
+    try:
+        for seed in (12345, 3):
+            e_d, c_d, f_d, s_d = g.build_rabitq(seed)
+            e_h, c_h, f_h, s_h = host.build_rabitq(base, edges, seed)
+            assert e_d == e_h
+            assert np.array_equal(c_d, c_h)
+            assert s_d.tobytes() == s_h.tobytes()
+            bad = np.nonzero(f_d.view(np.uint32) != f_h.view(np.uint32))
+            assert len(bad[0]) == 0, (dim, seed, bad[0][:5], bad[1][:5])
+    finally:
+        g.close()
+
+
+@pytest.mark.parametrize("name", ["d32", "d100"])
+def test_device_rabitq_codebook_reference_file(gpu, name):
+    """the codebook file written from the device build has the sha256 of the reference
+    build_rabitq's file for the same graph"""
+    import hashlib, json, os, tempfile
+    golden = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+    meta = json.load(open(os.path.join(golden, f"build_{name}.json")))
+    spec = meta["spec"]
+    if spec["kind"] == "mixture":
+        base = host.gen_mixture(spec["n"], spec["dim"], spec["centres"], 0.0, 128.0, 12.0, 0.0, 101, 202)
+    else:
+        base = host.gen_normalized(spec["n"], spec["dim"], 202)
+    bg = meta["build_graph"]
+    edges = host.build_vamana(base, bg["degree"], bg["beam"], bg["alpha"], bg["seed"], exact=True, threads=4)
+    g = search.GPUGraph(base, edges)
+    try:
+        entry, codes, factors, signs = g.build_rabitq(meta["build_rabitq"]["seed"])
+    finally:
+        g.close()
+    d = tempfile.mkdtemp()
+    host.write_codebook(f"{d}/cb.bin", base, edges, entry, codes, factors, signs)
+    assert hashlib.sha256(open(f"{d}/cb.bin", "rb").read()).hexdigest() == meta["codebook_sha256"]
