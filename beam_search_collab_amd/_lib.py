@@ -60,6 +60,7 @@ HIP_API = {
     "bs_index_set_query_order": (C.c_int, [vp, C.c_int]),
     "bs_index_entry_point": (C.c_int, [vp, P(u32)]),
     "bs_index_build_rabitq": (C.c_int, [vp, u32, vp, vp, vp, P(u32)]),
+    "bs_build_vamana_device": (C.c_int, [vp, u64, u32, u32, u32, f32, u32, vp, C.c_int]),
     "bs_last_error": (C.c_char_p, []),
     "bs_debug_l2": (C.c_int, [vp, vp, u64, vp, vp, u64, vp]),
     "bs_debug_fastscan": (C.c_int, [vp, vp, u32, u32, vp, vp, u32, u32, f32, vp, vp, vp, vp, vp]),

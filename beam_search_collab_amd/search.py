@@ -186,6 +186,20 @@ class GPUGraph:
         return st.as_dict()
 
 
+def build_vamana_device(vecs: np.ndarray, degree: int = 32, beam_width: int = 128, alpha: float = 2.0,
+                        seed: int = 1234, verbose: bool = False) -> np.ndarray:
+    """build_graph (src/build_graph.cpp) on the device: the reference's graph, edge for
+    edge (host.build_vamana with exact=True gives the same rows)."""
+    v = np.ascontiguousarray(vecs, dtype=np.float32)
+    if v.ndim != 2:
+        raise ValueError("vecs must be n x dim")
+    n, dim = v.shape
+    edges = np.empty((n, degree), dtype=np.uint32)
+    _check(_lib.hip().bs_build_vamana_device(_ptr(v), n, dim, degree, beam_width, alpha, seed, _ptr(edges),
+                                             1 if verbose else 0), "bs_build_vamana_device")
+    return edges
+
+
 def make_cfg(mode: int, ny: int, K: int, cfg) -> _lib.SearchCfg:
     c = _lib.SearchCfg()
     c.mode = mode

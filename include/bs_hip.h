@@ -133,6 +133,17 @@ int bs_index_entry_point(bs_index idx, uint32_t* entry);
 int bs_index_build_rabitq(bs_index idx, uint32_t seed, uint32_t* codes, float* factors, float* signs,
                           uint32_t* entry);
 
+/* Vamana graph construction on the device: build_graph (src/build_graph.cpp:95-392) with
+ * the same insertion order (mt19937(seed) shuffle), batches, beam rule, sequential float
+ * distances, dedupe_and_prune and mirrored-edge order, so edges_out (host, n*degree u32,
+ * rows padded with node 0) equals the reference's graph (bs_build_vamana with exact != 0,
+ * bs_host.h).  vecs: host n*dim f32.  degree 1..128, beam_width 1..1024, alpha >= 1.
+ * Synchronous; allocates its work buffers (the visited bitmaps of up to 2 GiB, lists,
+ * visit lists and sort space).  Fails with BS_EINVAL if a search expands more than
+ * max(1024, 4*beam_width) nodes.  verbose != 0 prints progress to stderr. */
+int bs_build_vamana_device(const float* vecs, uint64_t n, uint32_t dim, uint32_t degree, uint32_t beam_width,
+                           float alpha, uint32_t seed, uint32_t* edges_out, int verbose);
+
 /* Device pointers of the uploaded index (for tests and profilers). */
 int bs_index_info(bs_index idx, uint64_t* n, uint32_t* dim, uint32_t* degree,
                   uint32_t* padded_dim, int* has_rabitq);

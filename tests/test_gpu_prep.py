@@ -105,3 +105,51 @@ def test_device_rabitq_codebook_reference_file(gpu, name):
     d = tempfile.mkdtemp()
     host.write_codebook(f"{d}/cb.bin", base, edges, entry, codes, factors, signs)
     assert hashlib.sha256(open(f"{d}/cb.bin", "rb").read()).hexdigest() == meta["codebook_sha256"]
+
+
+@pytest.mark.parametrize("n,dim,degree,beam,alpha,kind", [
+    (1, 8, 4, 8, 1.2, "mixture"), (7, 5, 4, 8, 1.0, "normalized"), (300, 24, 8, 16, 1.2, "mixture"),
+    (3000, 32, 16, 32, 2.0, "mixture"), (4000, 100, 32, 64, 1.2, "normalized"),
+    (5000, 128, 32, 128, 2.0, "mixture"), (2500, 48, 64, 100, 1.5, "normalized"),
+    (1500, 200, 24, 256, 2.0, "mixture"), (1200, 17, 128, 128, 1.2, "mixture")])
+def test_device_vamana_is_the_reference_graph(gpu, n, dim, degree, beam, alpha, kind):
+    """bs_build_vamana_device gives the host exact builder's rows (the host builder is
+    byte-identical to the reference build_graph), including tiny n, odd dims, degree 128
+    and beams that are not a multiple of 64"""
+    if kind == "mixture":
+        base = host.gen_mixture(n, dim, 6, 0.0, 50.0, 4.0, 0.0, n + dim, degree)
+    else:
+        base = host.gen_normalized(n, dim, n + degree)
+    for seed in (7, 1234):
+        want = host.build_vamana(base, degree, beam, alpha, seed, exact=True, threads=0)
+        got = search.build_vamana_device(base, degree, beam, alpha, seed)
+        bad = np.nonzero((got != want).any(1))[0]
+        assert len(bad) == 0, (n, dim, degree, seed, len(bad), bad[:5], got[bad[0]], want[bad[0]])
+
+
+def test_device_vamana_duplicate_points(gpu):
+    """repeated rows give equal distances: ties resolved by node id as the reference does"""
+    rng = np.random.default_rng(4)
+    base = rng.integers(0, 4, (2000, 16)).astype(np.float32)
+    want = host.build_vamana(base, 12, 32, 1.2, 5, exact=True, threads=0)
+    got = search.build_vamana_device(base, 12, 32, 1.2, 5)
+    assert np.array_equal(got, want)
+
+
+@pytest.mark.parametrize("name", ["d32", "d100"])
+def test_device_vamana_reference_file(gpu, name):
+    """the graph file written from the device build has the sha256 of the reference
+    build_graph's file"""
+    import hashlib, json, os, tempfile
+    golden = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+    meta = json.load(open(os.path.join(golden, f"build_{name}.json")))
+    spec = meta["spec"]
+    if spec["kind"] == "mixture":
+        base = host.gen_mixture(spec["n"], spec["dim"], spec["centres"], 0.0, 128.0, 12.0, 0.0, 101, 202)
+    else:
+        base = host.gen_normalized(spec["n"], spec["dim"], 202)
+    bg = meta["build_graph"]
+    edges = search.build_vamana_device(base, bg["degree"], bg["beam"], bg["alpha"], bg["seed"])
+    d = tempfile.mkdtemp()
+    host.write_graph(f"{d}/g.bin", edges)
+    assert hashlib.sha256(open(f"{d}/g.bin", "rb").read()).hexdigest() == meta["graph_sha256"]
