@@ -295,7 +295,7 @@ def main():
 
     assert torch.cuda.is_available(), "bench.py needs the GPU"
     dev = torch.device("cuda:0")
-    cache = os.path.join(args.cache, f"bench_{args.data}_{args.n}x{args.dim}_{args.nq}q_R{args.degree}.npz") if args.cache else ""
+    cache = os.path.join(args.cache, f"bench_{args.data}_{args.n}x{args.dim}_{args.nq}q_R{args.degree}_ref.npz") if args.cache else ""
     if cache and os.path.exists(cache):
         z = np.load(cache)
         base, queries, edges, gt = z["base"], z["queries"], z["edges"], z["gt"]
@@ -307,8 +307,9 @@ def main():
         log(f"config {args.config}: data {args.n}x{args.dim} ({args.data}), {args.nq} queries: "
             f"{time.time() - t0:.1f}s")
         t1 = time.time()
-        edges = host.build_vamana(base, args.degree, 128, 2.0, 1234, exact=False, verbose=True)
-        log(f"Vamana graph R={args.degree}: {time.time() - t1:.1f}s")
+        # the reference build_graph's graph, built on the device (bs_build_vamana_device)
+        edges = search.build_vamana_device(base, args.degree, 128, 2.0, 1234)
+        log(f"Vamana graph R={args.degree} on the device (bs_build_vamana_device): {time.time() - t1:.1f}s")
         t1 = time.time()
         q_t = torch.from_numpy(queries).to(dev)
         if args.dim <= 256:
