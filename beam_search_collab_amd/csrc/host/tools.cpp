@@ -1,10 +1,11 @@
 // build_graph / build_rabitq / gen_data / compute_gt command-line tools (one binary per
 // tool, selected at compile time with -DBS_TOOL=...).
 //   build_graph  --base B.fvecs --graph G.bin [--degree 32] [--beam-width 128] [--alpha 2.0]
-//                [--metric l2] [--seed 1234] [--threads N] [--fast]
-//                (flags of src/build_graph.cpp:210-256; --fast uses vectorized distances)
-//   build_rabitq -base B.fvecs -graph G.bin -out CB.bin [-seed 12345]
-//                (flags of src/build_rabitq.cpp:103-120)
+//                [--metric l2] [--seed 1234] [--threads N] [--fast] [--device]
+//                (flags of src/build_graph.cpp:210-256; --fast uses vectorized distances,
+//                --device builds the same graph as the default on the GPU)
+//   build_rabitq -base B.fvecs -graph G.bin -out CB.bin [-seed 12345] [-device]
+//                (flags of src/build_rabitq.cpp:103-120; -device: the same codebook from the GPU)
 //   gen_data     --out-base B.fvecs --out-query Q.fvecs --n N --nq Q --dim D
 //                [--kind mixture|normalized] [--centres 64] [--lo 0] [--hi 128] [--sigma 12]
 //   compute_gt   --base B.fvecs --query Q.fvecs --out GT.ivecs [--k 100]
@@ -12,6 +13,9 @@
 //                (positional arguments of src/replicate_queries.cpp:10-24; writes the input
 //                rows `repeats` times in order, for larger query batches)
 #include "bs_host.h"
+#if BS_TOOL == 1 || BS_TOOL == 2
+#include "bs_hip.h"
+#endif
 
 #include <chrono>
 #include <cmath>
@@ -58,10 +62,10 @@ double now() { return std::chrono::duration<double>(std::chrono::steady_clock::n
 int main(int argc, char** argv) {
     try {
 #if BS_TOOL == 1
-        auto a = args(argc, argv, {"--fast", "--help"});
+        auto a = args(argc, argv, {"--fast", "--device", "--help"});
         if (a.count("--help")) {
             std::cout << "Usage: build_graph --base base.fvecs --graph graph.bin [--degree 32] [--beam-width 128]"
-                         " [--alpha 2.0] [--metric l2] [--seed 1234] [--threads N] [--fast]\n";
+                         " [--alpha 2.0] [--metric l2] [--seed 1234] [--threads N] [--fast] [--device]\n";
             return 0;
         }
         const std::string base = get(a, "--base", ""), graph = get(a, "--graph", "");
@@ -79,16 +83,22 @@ int main(int argc, char** argv) {
                   << " beam_width=" << beam << " alpha=" << alpha << " metric=l2\n";
         std::vector<uint32_t> edges(n * static_cast<uint64_t>(degree));
         const double t0 = now();
-        if (bs_build_vamana(static_cast<float*>(v.p), n, dim, degree, beam, static_cast<float>(alpha), seed,
-                            a.count("--fast") ? 0 : 1, std::stoi(get(a, "--threads", "0")), edges.data(), 1))
+        if (a.count("--device")) {
+            if (bs_build_vamana_device(static_cast<float*>(v.p), n, dim, degree, beam, static_cast<float>(alpha), seed,
+                                       edges.data(), 1))
+                throw std::runtime_error(bs_last_error());
+        } else if (bs_build_vamana(static_cast<float*>(v.p), n, dim, degree, beam, static_cast<float>(alpha), seed,
+                                   a.count("--fast") ? 0 : 1, std::stoi(get(a, "--threads", "0")), edges.data(), 1)) {
             throw std::runtime_error(bs_host_last_error());
+        }
         if (bs_write_graph(graph.c_str(), edges.data(), n, degree)) throw std::runtime_error(bs_host_last_error());
         std::cout << "Wrote graph to " << graph << "\nTotal build time: " << now() - t0 << "s\n";
 #elif BS_TOOL == 2
-        auto a = args(argc, argv, {});
+        auto a = args(argc, argv, {"-device"});
         const std::string base = get(a, "-base", ""), graph = get(a, "-graph", ""), out = get(a, "-out", "");
         if (base.empty() || graph.empty() || out.empty()) {
-            std::cerr << "Usage: " << argv[0] << " -base <base.fvecs> -graph <graph.bin> -out <codebook> [-seed <uint32>]\n";
+            std::cerr << "Usage: " << argv[0]
+                      << " -base <base.fvecs> -graph <graph.bin> -out <codebook> [-seed <uint32>] [-device]\n";
             return 1;
         }
         const uint32_t seed = static_cast<uint32_t>(std::stoul(get(a, "-seed", "12345")));
@@ -105,9 +115,19 @@ int main(int argc, char** argv) {
         std::vector<uint32_t> codes(n * degree * static_cast<uint64_t>(wpp));
         std::vector<float> factors(n * 3ull * degree), signs(pdim);
         uint32_t entry = 0;
-        if (bs_build_rabitq(static_cast<float*>(v.p), static_cast<uint32_t*>(e.p), n, dim, degree, seed, 0,
-                            codes.data(), factors.data(), signs.data(), &entry))
+        if (a.count("-device")) {
+            bs_index ix = nullptr;
+            if (bs_index_create(static_cast<float*>(v.p), static_cast<uint32_t*>(e.p), n, dim, degree, &ix) ||
+                bs_index_build_rabitq(ix, seed, codes.data(), factors.data(), signs.data(), &entry)) {
+                const std::string msg = bs_last_error();
+                bs_index_destroy(ix);
+                throw std::runtime_error(msg);
+            }
+            bs_index_destroy(ix);
+        } else if (bs_build_rabitq(static_cast<float*>(v.p), static_cast<uint32_t*>(e.p), n, dim, degree, seed, 0,
+                                   codes.data(), factors.data(), signs.data(), &entry)) {
             throw std::runtime_error(bs_host_last_error());
+        }
         std::cout << "Entry point (medoid): " << entry << "\n";
         if (bs_write_codebook(out.c_str(), static_cast<float*>(v.p), static_cast<uint32_t*>(e.p), n, dim, degree, entry,
                               codes.data(), factors.data(), signs.data(), pdim))

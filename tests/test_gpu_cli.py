@@ -70,3 +70,25 @@ def test_cli_config_errors(gpu, files):
     rc, _, err = run_cli({"data": {k: v for k, v in f.items() if k != "codebook"},
                           "search": {"mode": "rabitq", "K": 10, "topk_size": 64}})
     assert rc == 1 and "codebook" in err
+
+
+@pytest.mark.gpu
+def test_builder_clis_device_flags(files, tmp_path):
+    """build_graph --device and build_rabitq -device write the files the host paths write"""
+    import hashlib
+    f, _ = files
+    bindir = os.path.join(ROOT, "beam_search_collab_amd", "bin")
+    sha = lambda p: hashlib.sha256(open(p, "rb").read()).hexdigest()
+    g_host, g_dev = str(tmp_path / "g_host.bin"), str(tmp_path / "g_dev.bin")
+    for extra, out in (([], g_host), (["--device"], g_dev)):
+        p = subprocess.run([os.path.join(bindir, "build_graph"), "--base", f["base"], "--graph", out, "--degree", "24",
+                            "--beam-width", "48", "--alpha", "1.2", "--seed", "9"] + extra,
+                           capture_output=True, text=True, timeout=300)
+        assert p.returncode == 0, p.stderr
+    assert sha(g_host) == sha(g_dev)
+    c_host, c_dev = str(tmp_path / "c_host.bin"), str(tmp_path / "c_dev.bin")
+    for extra, out in (([], c_host), (["-device"], c_dev)):
+        p = subprocess.run([os.path.join(bindir, "build_rabitq"), "-base", f["base"], "-graph", g_host, "-out", out,
+                            "-seed", "77"] + extra, capture_output=True, text=True, timeout=300)
+        assert p.returncode == 0, p.stderr
+    assert sha(c_host) == sha(c_dev)
