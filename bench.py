@@ -94,11 +94,11 @@ def gen_data(args):
 
 def gt_gpu(base_t, q_t, k, margin=28):
     """exact top-k for dim > 256 (beyond bs_index_groundtruth), fp64 distances, ties by id
-    as bs_groundtruth: fp32 library-GEMM candidates
+    as bs_groundtruth: fp64 library-GEMM candidates
     on the GPU, exact fp64 re-scoring on the host, and a per-query certificate.
 
-    Candidate a_j = |b_j|^2 - 2 q.b_j (+ |q|^2) in fp32 differs from the exact distance by
-    at most eps = (dim + 3) * 2^-23 * (|q| + max|b|)^2 (dot-product and norm rounding, with a
+    Candidate a_j = |b_j|^2 - 2 q.b_j (+ |q|^2) in fp64 differs from the exact distance by
+    at most eps = (dim + 3) * 2^-52 * (|q| + max|b|)^2 (dot-product and norm rounding, with a
     factor 2 to spare).  Every row outside the kk candidates has a_j >= a_kk (the chunked
     selection keeps that invariant), so when the exact k-th distance among the candidates
     is below a_kk - eps no other row can enter the top k.  Queries that fail the test are
@@ -108,9 +108,11 @@ def gt_gpu(base_t, q_t, k, margin=28):
     from beam_search_collab_amd import host
     nq, dim = q_t.shape
     kk = k + margin
+    base_t = base_t.double()
+    q_t = q_t.double()
     bn = (base_t * base_t).sum(1)
     cand = torch.empty((nq, kk), dtype=torch.int64, device=q_t.device)
-    akk = torch.empty(nq, dtype=torch.float32, device=q_t.device)
+    akk = torch.empty(nq, dtype=torch.float64, device=q_t.device)
     for i in range(0, nq, 1024):
         q = q_t[i:i + 1024]
         best_d = None
@@ -129,13 +131,13 @@ def gt_gpu(base_t, q_t, k, margin=28):
                 best_d, best_i = v2, torch.gather(ci, 1, sel)
         cand[i:i + 1024] = best_i
         akk[i:i + 1024] = best_d.max(1).values
-    base = base_t.cpu().numpy()
-    queries = q_t.cpu().numpy()
+    base = base_t.float().cpu().numpy()
+    queries = q_t.float().cpu().numpy()
     gt = host.groundtruth_refine(base, queries, cand.cpu().numpy(), k)
     # certificate
     qn2 = (queries.astype(np.float64) ** 2).sum(1)
     bmax = float(np.sqrt(bn.max().item()))
-    eps = (dim + 3) * 2.0 ** -23 * (np.sqrt(qn2) + bmax) ** 2
+    eps = (dim + 3) * 2.0 ** -52 * (np.sqrt(qn2) + bmax) ** 2
     kth = gt[:, k - 1]
     dk = ((queries.astype(np.float64) - base[kth].astype(np.float64)) ** 2).sum(1)
     bad = np.nonzero(~(dk < akk.cpu().numpy().astype(np.float64) + qn2 - eps))[0]

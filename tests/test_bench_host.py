@@ -33,3 +33,15 @@ def test_configs_follow_the_survey():
     assert c["C"]["mode"] == "rabitq" and c["C"]["K"] == 10
     assert (c["D"]["n"], c["D"]["dim"], c["D"]["degree"], c["D"]["data"]) == (1_200_000, 100, 64, "normal")
     assert (c["E"]["dim"], c["E"]["nq"], c["E"]["data"]) == (960, 1_000, "mix256")
+
+
+def test_high_dim_ground_truth_candidates_and_certificate():
+    """bench.gt_gpu (the ground truth above dim 256: fp64 GEMM candidates, host re-score,
+    certificate) equals the host brute force; run here on CPU tensors, with clustered data
+    whose k-th and (k+1)-th distances are close"""
+    import torch
+    from beam_search_collab_amd import host
+    base = host.gen_mixture(3000, 300, 8, 0.0, 1.0, 0.05, 0.0, 5, 6)
+    q = host.gen_mixture(40, 300, 8, 0.0, 1.0, 0.05, 0.0, 5, 7)
+    got = bench.gt_gpu(torch.from_numpy(base), torch.from_numpy(q), 20, margin=8)
+    assert np.array_equal(got, host.groundtruth(base, q, 20))
