@@ -40,7 +40,8 @@ struct SearchParams {
 };
 
 template <int TR, int CR, int QMAX, int MODE, int PB>
-__global__ void __launch_bounds__(512) search_kernel(const SearchParams p) {
+__global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(MODE == MODE_RABITQ && TR <= 4 && CR == 1 ? 5 : 1, 8)))
+search_kernel(const SearchParams p) {
     extern __shared__ __attribute__((aligned(16))) char smem[];
     const uint32_t lane = lane_id();
     const uint32_t wave = threadIdx.x >> 6;
