@@ -362,7 +362,7 @@ int make_plan(bs_index ix, const bs_search_cfg* cfg, uint64_t nq, Plan& pl) {
     if (cap > (1u << 22)) return fail(BS_EINVAL, "filter_capacity must be <= 2^22");
 
     pl.mode = mode;
-    pl.TR = T <= 64 ? 1 : T <= 128 ? 2 : T <= 256 ? 4 : T <= 512 ? 8 : 16;
+    pl.TR = T <= 64 ? 1 : T <= 128 ? 2 : T <= 256 ? 4 : T <= 512 ? 8 : (T <= 768 && mode == BS_RABITQ) ? 12 : 16;
     pl.CR = ix->degree <= 64 ? 1 : 2;
     bsd::L2Shape L = bsd::l2_shape(ix->dim);
     if (L.QR > 4) return fail(BS_EINVAL, "dim too large");

@@ -302,6 +302,23 @@ __device__ __forceinline__ void bitonic_sort(uint64_t (&v)[TR]) {
     }
 }
 
+// the same for any register count: counts that are not a power of two sort in the next
+// power of two, padded with EMPTY keys (which sort last)
+template <int TR>
+__device__ __forceinline__ void sort_beam(uint64_t (&v)[TR]) {
+    if constexpr ((TR & (TR - 1)) == 0) {
+        bitonic_sort<TR>(v);
+    } else {
+        constexpr int P = TR <= 16 ? 16 : 32;
+        uint64_t w[P];
+#pragma unroll
+        for (int r = 0; r < P; ++r) w[r] = r < TR ? v[r] : EMPTY_KEY;
+        bitonic_sort<P>(w);
+#pragma unroll
+        for (int r = 0; r < TR; ++r) v[r] = w[r];
+    }
+}
+
 // ---------------------------------------------------------------------------
 // visit filters in the wave's LDS slice
 // ---------------------------------------------------------------------------

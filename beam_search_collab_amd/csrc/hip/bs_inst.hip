@@ -51,6 +51,9 @@ static hipError_t launch_any(const SearchParams& p, int TR, int CR, int PB, dim3
     case 2: return launch_c<2>(p, CR, PB, g, b, lds, s);
     case 4: return launch_c<4>(p, CR, PB, g, b, lds, s);
     case 8: return launch_c<8>(p, CR, PB, g, b, lds, s);
+#if BS_INST_MODE >= 2
+    case 12: return launch_c<12>(p, CR, PB, g, b, lds, s);  // rabitq beams of 513..768
+#endif
     default: return launch_c<16>(p, CR, PB, g, b, lds, s);
     }
 }

@@ -241,12 +241,14 @@ def cpu_baseline(files, nq_total, args):
 
 
 def kernel_name(mode, topk, degree, dim):
-    """symbol of the search-kernel instance a launch uses (beam registers TR = topk/64,
+    """symbol of the search-kernel instance a launch uses (beam registers TR = topk/64 rounded
+    up to 1, 2, 4, 8, 16, or 12 for rabitq beams of 513..768,
     candidate registers CR = degree/64, 4 float4 chunks per lane, filter/mode id, row
     passes in flight PB from the L2 row shape)"""
-    tr = 1 if topk <= 64 else 2 if topk <= 128 else 4 if topk <= 256 else 8 if topk <= 512 else 16
-    cr = 1 if degree <= 64 else 2
     m = {"base": 0, "warp": 0, "bwarp": 1, "rabitq": 2}[mode.rstrip("0123456789")]
+    tr = 1 if topk <= 64 else 2 if topk <= 128 else 4 if topk <= 256 else 8 if topk <= 512 else \
+        12 if (topk <= 768 and m == 2) else 16
+    cr = 1 if degree <= 64 else 2
     p = 1
     while p < (dim + 3) // 4:
         p *= 2

@@ -25,6 +25,9 @@ def test_kernel_name_matches_instance_rules():
     assert bench.kernel_name("base", 512, 32, 960) == "bsd::search_kernel<8, 1, 4, 0, 8>"
     assert bench.kernel_name("rabitq", 256, 32, 128) == "bsd::search_kernel<4, 1, 4, 2, 2>"
     assert bench.kernel_name("rabitq", 256, 32, 960) == "bsd::search_kernel<4, 1, 4, 3, 8>"
+    # rabitq beams of 513..768 have a 12-register instance; the other modes use 16
+    assert bench.kernel_name("rabitq", 768, 32, 128) == "bsd::search_kernel<12, 1, 4, 2, 2>"
+    assert bench.kernel_name("base", 768, 32, 128) == "bsd::search_kernel<16, 1, 4, 0, 2>"
 
 
 def test_configs_follow_the_survey():

@@ -55,7 +55,7 @@ def assert_same(ids, d, st, oids, od, ost, ctx):
 
 
 @pytest.mark.parametrize("mode", ["base", "warp1", "warp2", "warp4", "warp8", "bwarp1", "bwarp4", "rabitq"])
-@pytest.mark.parametrize("topk", [16, 64, 100, 128, 256, 512, 1024])
+@pytest.mark.parametrize("topk", [16, 64, 100, 128, 256, 512, 600, 768, 1024])
 def test_modes_topk_d128(gpu, mode, topk):
     ds = dataset(4000, 128, 32, 64)
     K = min(10, topk)
