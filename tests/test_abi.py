@@ -38,3 +38,33 @@ def test_oracle_is_not_linked_by_the_product():
         if f.endswith(".py"):
             src = open(os.path.join(ROOT, "beam_search_collab_amd", f)).read()
             assert "oracle" not in src.replace("oracle/", "").lower() or f == "__init__.py", f
+
+
+def test_argument_errors_before_any_device_call():
+    """entry points reject bad arguments with BS_EINVAL and a message before they touch the
+    device (so this runs without a GPU)"""
+    C = ctypes
+    lib = _lib.hip()
+    h = C.c_void_p()
+    vecs = (C.c_float * 8)()
+    edges = (C.c_uint32 * 4)(1, 0xFFFFFFFF, 5, 0)  # node 2 would be out of range for n = 2
+    assert lib.bs_index_create(None, edges, 2, 4, 2, C.byref(h)) == -1
+    assert b"vecs and edges" in lib.bs_last_error()
+    assert lib.bs_index_create(vecs, edges, 2, 0, 2, C.byref(h)) == -1
+    assert b"dim" in lib.bs_last_error()
+    assert lib.bs_index_create(vecs, edges, 2, 4, 200, C.byref(h)) == -1
+    assert b"degree" in lib.bs_last_error()
+    assert lib.bs_index_create(vecs, edges, 2, 4, 2, C.byref(h)) == -1
+    assert b"points to node 5" in lib.bs_last_error()
+    assert lib.bs_index_create(vecs, edges, 2, 4, 2, None) == -1
+    cfg = _lib.SearchCfg(0, 1, 10, 64, 1024, 0, 1024, 16)
+    assert lib.bs_search_device(None, C.byref(cfg), None, 1, None, None, None, None, 0, None) == -1
+    assert lib.bs_index_set_query_order(None, 1) == -1
+    e = C.c_uint32()
+    assert lib.bs_index_entry_point(None, C.byref(e)) == -1
+    out = (C.c_uint32 * 4)()
+    assert lib.bs_build_vamana_device(vecs, 2, 4, 0, 8, 1.2, 1, out, 0) == -1
+    assert b"degree" in lib.bs_last_error()
+    assert lib.bs_build_vamana_device(vecs, 2, 4, 2, 8, 0.5, 1, out, 0) == -1
+    assert b"alpha" in lib.bs_last_error()
+    assert lib.bs_build_vamana_device(vecs, 0, 4, 2, 8, 1.2, 1, out, 0) == -1
