@@ -62,8 +62,8 @@ __device__ __forceinline__ uint32_t key_id(uint64_t k) { return static_cast<uint
 //    binary search of an LDS copy, the occupied output slots are marked in a bitmap and
 //    every output slot gathers its key from the candidate or the beam copy.
 // Identical keys are indistinguishable, so the two orders of equal candidates agree.
-// The sorted merge pays off where expansions add many candidates and registers are not
-// the occupancy limit (the RaBitQ loop); the base loop keeps the rank loop only.
+// Both loops use the sorted merge for one candidate register (degree <= 64); the kernels
+// that would lose a wavefront per SIMD to its registers are compiled for 5 waves per SIMD.
 // LDS: scratch = 64*TR keys, aux = 64 + TR keys.
 // ---------------------------------------------------------------------------
 // The rank loop costs ~(9 + 2 TR) instructions per candidate, the sorted merge a roughly

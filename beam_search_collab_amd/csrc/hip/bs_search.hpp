@@ -39,8 +39,11 @@ struct SearchParams {
     L2Shape L;
 };
 
+// Beams up to 256 with one candidate register and rows of at most 128 dims (PB = 2; the
+// RaBitQ loop always) are compiled for 5 wavefronts per SIMD (at most 96 VGPRs): the sorted
+// merge would otherwise take them to 4.
 template <int TR, int CR, int QMAX, int MODE, int PB>
-__global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(MODE == MODE_RABITQ && TR <= 4 && CR == 1 ? 5 : 1, 8)))
+__global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu((MODE == MODE_RABITQ || PB == 2) && TR <= 4 && CR == 1 ? 5 : 1, 8)))
 search_kernel(const SearchParams p) {
     extern __shared__ __attribute__((aligned(16))) char smem[];
     const uint32_t lane = lane_id();
@@ -135,7 +138,7 @@ search_kernel(const SearchParams p) {
             bool any = false;
 #pragma unroll
             for (int rc = 0; rc < CR; ++rc) any = any || (cm[rc] != 0);
-            if (any) beam_merge<TR, CR, false>(beam, ck, cm, T, scratch, merge_aux);
+            if (any) beam_merge<TR, CR, (CR == 1)>(beam, ck, cm, T, scratch, merge_aux);
 #pragma unroll
             for (int rc = 0; rc < CR; ++rc) cm[rc] = 0;
 
@@ -214,7 +217,7 @@ search_kernel(const SearchParams p) {
             bool any = false;
 #pragma unroll
             for (int rc = 0; rc < CR; ++rc) any = any || (cm[rc] != 0);
-            if (any) beam_merge<TR, CR, false>(beam, ck, cm, T, scratch, merge_aux);
+            if (any) beam_merge<TR, CR, (CR == 1)>(beam, ck, cm, T, scratch, merge_aux);
         }
         // flush the K smallest, ascending
         uint32_t* out = p.results + qid * p.K;
