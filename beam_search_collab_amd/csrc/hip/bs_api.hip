@@ -10,6 +10,8 @@
 #include <cfloat>
 #include <cstdio>
 #include <cstring>
+#include <exception>
+#include <new>
 #include <string>
 #include <vector>
 
@@ -138,9 +140,22 @@ int bs_internal_edges(bs_index ix, const uint32_t** edges) {
     return BS_OK;
 }
 void bs_internal_set_error(const std::string& msg) { g_err = msg; }
+// Inside a catch handler: the error code and text for the exception in flight (every
+// entry point catches all exceptions; none crosses the C-ABI).
+int bs_internal_exception() {
+    try {
+        throw;
+    } catch (const std::bad_alloc&) {
+        return fail(BS_ENOMEM, "host memory allocation failed");
+    } catch (const std::exception& e) {
+        return fail(BS_EHIP, std::string("internal error: ") + e.what());
+    } catch (...) {
+        return fail(BS_EHIP, "internal error");
+    }
+}
 
 extern "C" int bs_index_create(const float* vecs, const uint32_t* edges, uint64_t n, uint32_t dim,
-                               uint32_t degree, bs_index* out) {
+                               uint32_t degree, bs_index* out) try {
     if (!out) return fail(BS_EINVAL, "out is null");
     *out = nullptr;
     if (!vecs || !edges) return fail(BS_EINVAL, "vecs and edges must be given");
@@ -211,6 +226,8 @@ extern "C" int bs_index_create(const float* vecs, const uint32_t* edges, uint64_
     }
     *out = ix;
     return BS_OK;
+} catch (...) {
+    return bs_internal_exception();
 }
 
 // Node records [vec dstride | ids R | tx R | fdq R | fvq R | codes R*cws | 0...] (rw words),
@@ -239,7 +256,7 @@ __global__ void __launch_bounds__(256) assemble_records(const float* vecs, const
 }
 
 extern "C" int bs_index_attach_rabitq(bs_index ix, const uint32_t* codes, const float* factors,
-                                      const float* signs, uint32_t padded_dim) {
+                                      const float* signs, uint32_t padded_dim) try {
     if (!ix || !codes || !factors || !signs) return fail(BS_EINVAL, "null argument");
     uint32_t p = 1;
     while (p < ix->dim) p <<= 1;
@@ -294,10 +311,12 @@ extern "C" int bs_index_attach_rabitq(bs_index ix, const uint32_t* codes, const 
     (void)hipFree(d_fac);
     if (e != hipSuccess) return fail(BS_EHIP, std::string("rabitq record assembly: ") + hipGetErrorString(e));
     return BS_OK;
+} catch (...) {
+    return bs_internal_exception();
 }
 
 extern "C" int bs_index_info(bs_index ix, uint64_t* n, uint32_t* dim, uint32_t* degree,
-                             uint32_t* padded_dim, int* has_rabitq) {
+                             uint32_t* padded_dim, int* has_rabitq) try {
     if (!ix) return fail(BS_EINVAL, "null index");
     if (n) *n = ix->n;
     if (dim) *dim = ix->dim;
@@ -305,6 +324,8 @@ extern "C" int bs_index_info(bs_index ix, uint64_t* n, uint32_t* dim, uint32_t* 
     if (padded_dim) *padded_dim = ix->pdim;
     if (has_rabitq) *has_rabitq = ix->d_recs != nullptr;
     return BS_OK;
+} catch (...) {
+    return bs_internal_exception();
 }
 
 extern "C" void bs_index_destroy(bs_index ix) {
@@ -323,11 +344,13 @@ extern "C" void bs_index_destroy(bs_index ix) {
     delete ix;
 }
 
-extern "C" int bs_index_set_query_order(bs_index ix, int mode) {
+extern "C" int bs_index_set_query_order(bs_index ix, int mode) try {
     if (!ix) return fail(BS_EINVAL, "null index");
     if (mode < 0 || mode > 2) return fail(BS_EINVAL, "query order mode must be 0, 1 or 2");
     ix->order_mode = mode;
     return BS_OK;
+} catch (...) {
+    return bs_internal_exception();
 }
 
 namespace {
@@ -496,7 +519,7 @@ hipError_t launch_ordered(bs_index ix, Plan pl, uint64_t nq, hipStream_t s) {
 
 extern "C" int bs_search_device(bs_index ix, const bs_search_cfg* cfg, const float* d_queries, uint64_t nq,
                                 uint32_t* d_results, float* d_dists, uint32_t* d_per_query, void* stream,
-                                int sync, bs_stats* stats) {
+                                int sync, bs_stats* stats) try {
     Plan pl;
     int rc = make_plan(ix, cfg, nq, pl);
     if (rc) return rc;
@@ -547,10 +570,12 @@ extern "C" int bs_search_device(bs_index ix, const bs_search_cfg* cfg, const flo
         }
     }
     return BS_OK;
+} catch (...) {
+    return bs_internal_exception();
 }
 
 extern "C" int bs_search(bs_index ix, const bs_search_cfg* cfg, const float* queries, uint64_t nq,
-                         uint32_t* results, float* dists, bs_stats* stats) {
+                         uint32_t* results, float* dists, bs_stats* stats) try {
     Plan pl;
     int rc = make_plan(ix, cfg, nq, pl);
     if (rc) return rc;
@@ -590,4 +615,6 @@ extern "C" int bs_search(bs_index ix, const bs_search_cfg* cfg, const float* que
     cleanup();
     if (rc == BS_OK && stats) *stats = st;
     return rc;
+} catch (...) {
+    return bs_internal_exception();
 }

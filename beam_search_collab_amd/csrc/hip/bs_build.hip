@@ -40,6 +40,7 @@
 #include <vector>
 
 void bs_internal_set_error(const std::string& msg);
+int bs_internal_exception();
 
 namespace bvb {
 
@@ -468,7 +469,7 @@ struct DevBuf {
 
 extern "C" int bs_build_vamana_device(const float* vecs, uint64_t n, uint32_t dim, uint32_t degree,
                                       uint32_t beam_width, float alpha, uint32_t seed, uint32_t* edges_out,
-                                      int verbose) {
+                                      int verbose) try {
     if (!vecs || !edges_out) return vfail(BS_EINVAL, "vecs and edges_out must be given");
     if (n == 0) return vfail(BS_EINVAL, "base dataset is empty");
     if (n > 0x7FFFFFFFull) return vfail(BS_EINVAL, "at most 2^31-1 points");
@@ -658,4 +659,6 @@ extern "C" int bs_build_vamana_device(const float* vecs, uint64_t n, uint32_t di
     if (e == hipSuccess) e = hipMemcpy(edges_out, d_edges.p, n * degree * 4ull, hipMemcpyDeviceToHost);
     if (e != hipSuccess) return vfail(BS_EHIP, std::string("graph construction: ") + hipGetErrorString(e));
     return BS_OK;
+} catch (...) {
+    return bs_internal_exception();
 }

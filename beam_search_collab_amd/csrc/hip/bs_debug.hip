@@ -42,6 +42,7 @@ extern "C" int bs_index_info(bs_index idx, uint64_t* n, uint32_t* dim, uint32_t*
                              int* has_rabitq);
 int bs_internal_vecs(bs_index idx, const float** vecs, uint32_t* dstride);
 void bs_internal_set_error(const std::string& msg);
+int bs_internal_exception();
 
 namespace {
 int dfail(int code, const std::string& msg) {
@@ -68,7 +69,7 @@ __global__ void __launch_bounds__(256) dbg_l2_kernel(const float* vecs, uint32_t
 }
 
 extern "C" int bs_debug_l2(bs_index idx, const float* queries, uint64_t nq, const uint32_t* qi,
-                           const uint32_t* ni, uint64_t npairs, float* out) {
+                           const uint32_t* ni, uint64_t npairs, float* out) try {
     uint64_t n = 0;
     uint32_t dim = 0, degree = 0;
     int rc = bs_index_info(idx, &n, &dim, &degree, nullptr, nullptr);
@@ -95,6 +96,8 @@ extern "C" int bs_debug_l2(bs_index idx, const float* queries, uint64_t nq, cons
     DTRY(hipGetLastError());
     DTRY(hipMemcpy(out, dout.p, npairs * 4, hipMemcpyDeviceToHost));
     return BS_OK;
+} catch (...) {
+    return bs_internal_exception();
 }
 
 // ---------------------------------------------------------------------------
@@ -148,7 +151,7 @@ __global__ void __launch_bounds__(64) dbg_fastscan_kernel(const float* query, co
 extern "C" int bs_debug_fastscan(const float* query, const float* signs, uint32_t dim, uint32_t seed,
                                  const uint32_t* codes_nbr, const float* factors, uint32_t nn, uint32_t degree,
                                  float exact, uint8_t* codes_out, float* scal_out, int32_t* sum_q_out,
-                                 uint32_t* raw_out, float* est_out) {
+                                 uint32_t* raw_out, float* est_out) try {
     uint32_t pdim = 1;
     while (pdim < dim) pdim <<= 1;
     if (pdim < 32 || pdim > 2048) return dfail(BS_EINVAL, "padded dim must be in 32..2048");
@@ -185,6 +188,8 @@ extern "C" int bs_debug_fastscan(const float* query, const float* signs, uint32_
     DTRY(hipMemcpy(raw_out, draw.p, nn * 4, hipMemcpyDeviceToHost));
     DTRY(hipMemcpy(est_out, dest.p, nn * 4, hipMemcpyDeviceToHost));
     return BS_OK;
+} catch (...) {
+    return bs_internal_exception();
 }
 
 // ---------------------------------------------------------------------------
@@ -240,7 +245,7 @@ static void launch_beam_c(int CR, int run, uint32_t T, const uint64_t* k, uint32
 }
 
 extern "C" int bs_debug_beam(uint32_t topk, const uint64_t* keys, uint32_t nbatch, uint32_t bsize, uint32_t picks,
-                             int pick_run, uint32_t* picked, uint64_t* beam_out) {
+                             int pick_run, uint32_t* picked, uint64_t* beam_out) try {
     if (topk == 0 || topk > 1024) return dfail(BS_EINVAL, "topk must be in 1..1024");
     if (bsize == 0 || bsize > 128) return dfail(BS_EINVAL, "bsize must be in 1..128");
     DevBuf<uint64_t> dk, db;
@@ -263,6 +268,8 @@ extern "C" int bs_debug_beam(uint32_t topk, const uint64_t* keys, uint32_t nbatc
     DTRY(hipMemcpy(beam_out, db.p, topk * 8, hipMemcpyDeviceToHost));
     if (nbatch * picks) DTRY(hipMemcpy(picked, dp.p, static_cast<size_t>(nbatch) * picks * 4, hipMemcpyDeviceToHost));
     return BS_OK;
+} catch (...) {
+    return bs_internal_exception();
 }
 
 // ---------------------------------------------------------------------------
@@ -285,7 +292,7 @@ __global__ void __launch_bounds__(64) dbg_sort_kernel(const uint64_t* keys, uint
     }
 }
 
-extern "C" int bs_debug_sort(const uint64_t* keys, uint32_t n, uint64_t* out) {
+extern "C" int bs_debug_sort(const uint64_t* keys, uint32_t n, uint64_t* out) try {
     if (n == 0) return BS_OK;
     if (n > 1024) return dfail(BS_EINVAL, "n must be <= 1024");
     DevBuf<uint64_t> dk, dout;
@@ -300,6 +307,8 @@ extern "C" int bs_debug_sort(const uint64_t* keys, uint32_t n, uint64_t* out) {
     DTRY(hipGetLastError());
     DTRY(hipMemcpy(out, dout.p, n * 8, hipMemcpyDeviceToHost));
     return BS_OK;
+} catch (...) {
+    return bs_internal_exception();
 }
 
 // ---------------------------------------------------------------------------
@@ -342,7 +351,7 @@ __global__ void __launch_bounds__(64) dbg_filter_kernel(int bloom, uint32_t bits
 }
 
 extern "C" int bs_debug_filter(int bloom, uint32_t capacity, const uint32_t* keys, uint32_t nbatch, uint32_t bsize,
-                               uint32_t* out_new, const uint32_t* qkeys, uint32_t nquery, uint32_t* out_contains) {
+                               uint32_t* out_new, const uint32_t* qkeys, uint32_t nquery, uint32_t* out_contains) try {
     if (bsize == 0 || bsize > 64) return dfail(BS_EINVAL, "bsize must be in 1..64");
     uint32_t bits = 0;
     while ((1ull << bits) < capacity) ++bits;
@@ -368,4 +377,6 @@ extern "C" int bs_debug_filter(int bloom, uint32_t capacity, const uint32_t* key
     if (nk) DTRY(hipMemcpy(out_new, dn.p, nk * 4, hipMemcpyDeviceToHost));
     if (nquery) DTRY(hipMemcpy(out_contains, dc.p, nquery * 4, hipMemcpyDeviceToHost));
     return BS_OK;
+} catch (...) {
+    return bs_internal_exception();
 }

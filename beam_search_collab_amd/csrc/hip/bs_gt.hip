@@ -24,6 +24,7 @@
 
 int bs_internal_vecs(bs_index idx, const float** vecs, uint32_t* dstride);
 void bs_internal_set_error(const std::string& msg);
+int bs_internal_exception();
 
 namespace bsg {
 
@@ -319,7 +320,7 @@ hipError_t launch_select(dim3 g, hipStream_t s, const float* vecs, uint32_t dstr
 
 extern "C" int bs_index_groundtruth_device(bs_index idx, const float* d_queries, uint64_t nq, uint32_t k,
                                            int32_t* d_out, uint8_t* d_uncertified, void* stream,
-                                           uint64_t* n_uncertified) {
+                                           uint64_t* n_uncertified) try {
     const float* vecs = nullptr;
     uint32_t dstride = 0;
     int rc = bs_internal_vecs(idx, &vecs, &dstride);
@@ -389,10 +390,12 @@ extern "C" int bs_index_groundtruth_device(bs_index idx, const float* d_queries,
     if (e != hipSuccess) return gfail(BS_EHIP, std::string("ground truth: ") + hipGetErrorString(e));
     if (n_uncertified) *n_uncertified = nu;
     return BS_OK;
+} catch (...) {
+    return bs_internal_exception();
 }
 
 extern "C" int bs_index_groundtruth(bs_index idx, const float* queries, uint64_t nq, uint32_t k, int32_t* out,
-                                    uint8_t* uncertified, uint64_t* n_uncertified) {
+                                    uint8_t* uncertified, uint64_t* n_uncertified) try {
     if (nq == 0) {
         if (n_uncertified) *n_uncertified = 0;
         return BS_OK;
@@ -426,9 +429,11 @@ extern "C" int bs_index_groundtruth(bs_index idx, const float* queries, uint64_t
     }
     release();
     return rc;
+} catch (...) {
+    return bs_internal_exception();
 }
 
-extern "C" int bs_debug_mfma32(const float* A, const float* B, float* D) {
+extern "C" int bs_debug_mfma32(const float* A, const float* B, float* D) try {
     float *dA = nullptr, *dB = nullptr, *dD = nullptr;
     auto release = [&]() {
         if (dA) (void)hipFree(dA);
@@ -450,4 +455,6 @@ extern "C" int bs_debug_mfma32(const float* A, const float* B, float* D) {
     release();
     if (e != hipSuccess) return gfail(BS_EHIP, std::string("mfma check: ") + hipGetErrorString(e));
     return BS_OK;
+} catch (...) {
+    return bs_internal_exception();
 }

@@ -27,6 +27,7 @@
 int bs_internal_vecs(bs_index idx, const float** vecs, uint32_t* dstride);
 int bs_internal_edges(bs_index idx, const uint32_t** edges);
 void bs_internal_set_error(const std::string& msg);
+int bs_internal_exception();
 
 namespace bsp {
 
@@ -257,7 +258,7 @@ int pfail(int code, const std::string& msg) {
 }
 }  // namespace
 
-extern "C" int bs_index_entry_point(bs_index idx, uint32_t* entry) {
+extern "C" int bs_index_entry_point(bs_index idx, uint32_t* entry) try {
     if (!entry) return pfail(BS_EINVAL, "entry is null");
     const float* vecs = nullptr;
     uint32_t dstride = 0;
@@ -294,10 +295,12 @@ extern "C" int bs_index_entry_point(bs_index idx, uint32_t* entry) {
     if (e != hipSuccess) return pfail(BS_EHIP, std::string("entry point: ") + hipGetErrorString(e));
     *entry = static_cast<uint32_t>(key & 0xFFFFFFFFull);
     return BS_OK;
+} catch (...) {
+    return bs_internal_exception();
 }
 
 extern "C" int bs_index_build_rabitq(bs_index idx, uint32_t seed, uint32_t* codes_out, float* factors_out,
-                                     float* signs_out, uint32_t* entry_out) {
+                                     float* signs_out, uint32_t* entry_out) try {
     if (!codes_out || !factors_out || !signs_out || !entry_out) return pfail(BS_EINVAL, "null output");
     const float* vecs = nullptr;
     const uint32_t* edges = nullptr;
@@ -421,4 +424,6 @@ extern "C" int bs_index_build_rabitq(bs_index idx, uint32_t seed, uint32_t* code
     for (uint32_t t = 0; t < T; ++t) pool.emplace_back(finish, n * t / T, n * (t + 1) / T);
     for (auto& th : pool) th.join();
     return BS_OK;
+} catch (...) {
+    return bs_internal_exception();
 }

@@ -8,7 +8,9 @@
 #include <cmath>
 #include <cstdio>
 #include <cstring>
+#include <exception>
 #include <fstream>
+#include <new>
 #include <string>
 #include <unordered_set>
 #include <vector>
@@ -26,6 +28,18 @@ int fail(int code, const std::string& msg) {
 
 int n_threads(int threads) { return threads > 0 ? threads : omp_get_max_threads(); }
 
+int exception_code() {
+    try {
+        throw;
+    } catch (const std::bad_alloc&) {
+        return fail(BS_HOST_ENOMEM, "host memory allocation failed");
+    } catch (const std::exception& e) {
+        return fail(BS_HOST_EIO, std::string("internal error: ") + e.what());
+    } catch (...) {
+        return fail(BS_HOST_EIO, "internal error");
+    }
+}
+
 }  // namespace bsh
 
 using bsh::fail;
@@ -38,7 +52,7 @@ extern "C" void bs_host_free(void* p) { std::free(p); }
 // ---------------------------------------------------------------------------
 
 extern "C" int bs_read_vecs(const char* path, int is_int, void** data, uint64_t* n,
-                            uint32_t* dim) {
+                            uint32_t* dim) try {
     std::ifstream in(path, std::ios::binary);
     if (!in) return fail(BS_HOST_EIO, std::string("cannot open ") + path);
     in.seekg(0, std::ios::end);
@@ -85,10 +99,12 @@ extern "C" int bs_read_vecs(const char* path, int is_int, void** data, uint64_t*
     *n = rows;
     *dim = static_cast<uint32_t>(d);
     return BS_HOST_OK;
+} catch (...) {
+    return bsh::exception_code();
 }
 
 extern "C" int bs_write_vecs(const char* path, int is_int, const void* data, uint64_t n,
-                             uint32_t dim) {
+                             uint32_t dim) try {
     (void)is_int;
     std::ofstream out(path, std::ios::binary);
     if (!out) return fail(BS_HOST_EIO, std::string("cannot create ") + path);
@@ -107,9 +123,11 @@ extern "C" int bs_write_vecs(const char* path, int is_int, const void* data, uin
     }
     if (!out) return fail(BS_HOST_EIO, std::string("write failed: ") + path);
     return BS_HOST_OK;
+} catch (...) {
+    return bsh::exception_code();
 }
 
-extern "C" int bs_read_graph(const char* path, uint32_t** edges, uint64_t* n, uint32_t* degree) {
+extern "C" int bs_read_graph(const char* path, uint32_t** edges, uint64_t* n, uint32_t* degree) try {
     std::ifstream in(path, std::ios::binary);
     if (!in) return fail(BS_HOST_EIO, std::string("cannot open graph file: ") + path);
     in.seekg(0, std::ios::end);
@@ -131,9 +149,11 @@ extern "C" int bs_read_graph(const char* path, uint32_t** edges, uint64_t* n, ui
     *n = static_cast<uint64_t>(h[0]);
     *degree = static_cast<uint32_t>(h[1]);
     return BS_HOST_OK;
+} catch (...) {
+    return bsh::exception_code();
 }
 
-extern "C" int bs_write_graph(const char* path, const uint32_t* edges, uint64_t n, uint32_t degree) {
+extern "C" int bs_write_graph(const char* path, const uint32_t* edges, uint64_t n, uint32_t degree) try {
     std::ofstream out(path, std::ios::binary);
     if (!out) return fail(BS_HOST_EIO, std::string("cannot create ") + path);
     int32_t h[2] = {static_cast<int32_t>(n), static_cast<int32_t>(degree)};
@@ -141,6 +161,8 @@ extern "C" int bs_write_graph(const char* path, const uint32_t* edges, uint64_t 
     out.write(reinterpret_cast<const char*>(edges), static_cast<std::streamsize>(4 * n * degree));
     if (!out) return fail(BS_HOST_EIO, std::string("write failed: ") + path);
     return BS_HOST_OK;
+} catch (...) {
+    return bsh::exception_code();
 }
 
 extern "C" uint32_t bs_rabitq_padded_dim(uint32_t dim) {
@@ -151,7 +173,7 @@ extern "C" uint32_t bs_rabitq_padded_dim(uint32_t dim) {
 
 extern "C" int bs_read_codebook(const char* path, uint64_t n, uint32_t dim, uint32_t degree,
                                 uint32_t* entry, uint32_t** codes, float** factors,
-                                float** signs, uint32_t* padded_dim) {
+                                float** signs, uint32_t* padded_dim) try {
     const uint32_t pdim = bs_rabitq_padded_dim(dim);
     if (pdim < 32) return fail(BS_HOST_EINVAL, "rabitq needs a padded dim >= 32 (dim > 16)");
     const uint32_t wpp = pdim / 32;
@@ -201,12 +223,14 @@ extern "C" int bs_read_codebook(const char* path, uint64_t n, uint32_t dim, uint
     *signs = s;
     *padded_dim = pdim;
     return BS_HOST_OK;
+} catch (...) {
+    return bsh::exception_code();
 }
 
 extern "C" int bs_write_codebook(const char* path, const float* vecs, const uint32_t* edges,
                                  uint64_t n, uint32_t dim, uint32_t degree, uint32_t entry,
                                  const uint32_t* codes, const float* factors, const float* signs,
-                                 uint32_t padded_dim) {
+                                 uint32_t padded_dim) try {
     const uint32_t wpp = padded_dim / 32;
     const uint64_t code_off = dim, factor_off = code_off + uint64_t(wpp) * degree,
                    nbr_off = factor_off + 3ull * degree, row = nbr_off + degree;
@@ -224,6 +248,8 @@ extern "C" int bs_write_codebook(const char* path, const float* vecs, const uint
     out.write(reinterpret_cast<const char*>(signs), 4ll * padded_dim);
     if (!out) return fail(BS_HOST_EIO, std::string("write failed: ") + path);
     return BS_HOST_OK;
+} catch (...) {
+    return bsh::exception_code();
 }
 
 // ---------------------------------------------------------------------------
@@ -337,7 +363,7 @@ void gaussian_row(uint64_t stream, uint64_t row, uint32_t dim, double* z) {
 
 extern "C" int bs_gen_mixture(float* out, uint64_t n, uint32_t dim, uint32_t centres, float lo,
                               float hi, float sigma, float clamp_min, uint64_t seed_c,
-                              uint64_t seed_x) {
+                              uint64_t seed_x) try {
     if (centres == 0 || dim == 0) return fail(BS_HOST_EINVAL, "centres and dim must be positive");
     std::vector<float> C(static_cast<size_t>(centres) * dim);
     for (uint64_t i = 0; i < C.size(); ++i)
@@ -358,9 +384,11 @@ extern "C" int bs_gen_mixture(float* out, uint64_t n, uint32_t dim, uint32_t cen
         }
     }
     return BS_HOST_OK;
+} catch (...) {
+    return bsh::exception_code();
 }
 
-extern "C" int bs_gen_normalized(float* out, uint64_t n, uint32_t dim, uint64_t seed) {
+extern "C" int bs_gen_normalized(float* out, uint64_t n, uint32_t dim, uint64_t seed) try {
 #pragma omp parallel
     {
         std::vector<double> z(dim + 1);
@@ -375,6 +403,8 @@ extern "C" int bs_gen_normalized(float* out, uint64_t n, uint32_t dim, uint64_t 
         }
     }
     return BS_HOST_OK;
+} catch (...) {
+    return bsh::exception_code();
 }
 
 // ---------------------------------------------------------------------------
@@ -398,7 +428,7 @@ inline double l2d(const float* a, const float* b, uint32_t dim) {
 }  // namespace
 
 extern "C" int bs_groundtruth(const float* base, uint64_t n, const float* queries, uint64_t nq,
-                              uint32_t dim, uint32_t k, int32_t* out, int threads) {
+                              uint32_t dim, uint32_t k, int32_t* out, int threads) try {
     if (k == 0) return fail(BS_HOST_EINVAL, "k must be positive");
 #pragma omp parallel num_threads(bsh::n_threads(threads))
     {
@@ -425,11 +455,13 @@ extern "C" int bs_groundtruth(const float* base, uint64_t n, const float* querie
         }
     }
     return BS_HOST_OK;
+} catch (...) {
+    return bsh::exception_code();
 }
 
 extern "C" int bs_groundtruth_refine(const float* base, uint64_t n, const float* queries,
                                      uint64_t nq, uint32_t dim, const int64_t* cand,
-                                     uint32_t ncand, uint32_t k, int32_t* out, int threads) {
+                                     uint32_t ncand, uint32_t k, int32_t* out, int threads) try {
     if (k == 0 || ncand < k) return fail(BS_HOST_EINVAL, "need ncand >= k > 0");
 #pragma omp parallel num_threads(bsh::n_threads(threads))
     {
@@ -451,4 +483,6 @@ extern "C" int bs_groundtruth_refine(const float* base, uint64_t n, const float*
         }
     }
     return BS_HOST_OK;
+} catch (...) {
+    return bsh::exception_code();
 }

@@ -34,7 +34,7 @@ void wht(float* x, uint32_t n) {
 
 extern "C" int bs_build_rabitq(const float* vecs, const uint32_t* edges, uint64_t n, uint32_t dim,
                                uint32_t degree, uint32_t seed, int threads, uint32_t* codes_out,
-                               float* factors_out, float* signs_out, uint32_t* entry_out) {
+                               float* factors_out, float* signs_out, uint32_t* entry_out) try {
     const uint32_t pdim = bs_rabitq_padded_dim(dim);
     if (pdim < 32) return bsh::fail(BS_HOST_EINVAL, "rabitq needs a padded dim >= 32 (dim > 16)");
     const uint32_t wpp = pdim / 32;
@@ -147,4 +147,6 @@ extern "C" int bs_build_rabitq(const float* vecs, const uint32_t* edges, uint64_
         }
     }
     return BS_HOST_OK;
+} catch (...) {
+    return bsh::exception_code();
 }

@@ -205,7 +205,7 @@ void dedupe_and_prune(const Ctx& c, std::vector<Edge>& nb, uint32_t src, uint32_
 
 extern "C" int bs_build_vamana(const float* vecs, uint64_t n, uint32_t dim, uint32_t degree,
                                uint32_t beam_width, float alpha, uint32_t seed, int exact,
-                               int threads, uint32_t* edges_out, int verbose) {
+                               int threads, uint32_t* edges_out, int verbose) try {
     if (n == 0) return bsh::fail(BS_HOST_EINVAL, "base dataset is empty");
     if (degree == 0 || beam_width == 0) return bsh::fail(BS_HOST_EINVAL, "degree and beam width must be positive");
     if (!(alpha >= 1.0f)) return bsh::fail(BS_HOST_EINVAL, "alpha must be at least 1.0");
@@ -304,4 +304,6 @@ extern "C" int bs_build_vamana(const float* vecs, uint64_t n, uint32_t dim, uint
         for (size_t j = 0; j < degree; ++j) row[j] = j < lim ? graph[u][j].second : 0u;
     }
     return BS_HOST_OK;
+} catch (...) {
+    return bsh::exception_code();
 }
