@@ -441,10 +441,22 @@ int make_plan(bs_index ix, const bs_search_cfg* cfg, uint64_t nq, Plan& pl) {
     p.lds_wave = al(p.off_coop + 4u);
     // base mode with too few queries to give every SIMD 4 wavefronts: 2 or 4 wavefronts
     // share one query (the reference's block-per-query base kernel); they split the
-    // distance rows of each expansion, the rest of the loop runs on the first wavefront
+    // distance rows of each expansion, the rest of the loop runs on the first wavefront.
+    // Beams of 256 and more keep the first wavefront busy longer per expansion, so there
+    // the split is sized to keep every query resident (the instance's measured occupancy:
+    // 1M x 960, 1k queries, topk 256, 2 waves/SIMD: 4 wavefronts per query 8.2 ms, 2 per
+    // query 6.8 ms); smaller beams gain more from helpers than they lose to a second round
+    // of queries (topk 64 on the same data: 2.0 ms against 2.3 ms).
     p.coop = 1;
     if (mode == BS_BASE) {
-        const uint64_t slots = 16ull * ix->cus;
+        uint64_t slots = 16ull * ix->cus;
+        if (pl.TR >= 4) {
+            int w = 0;
+            if (bsd::launch_search_hash(p, pl.TR, pl.CR, pl.PB, dim3(1), dim3(64), p.lds_wave, nullptr, &w) ==
+                    hipSuccess &&
+                w > 0)
+                slots = static_cast<uint64_t>(w) * ix->cus;
+        }
         if (nq * 4 <= slots) p.coop = 4;
         else if (nq * 2 <= slots) p.coop = 2;
     }

@@ -9,9 +9,12 @@
 
 namespace bsd {
 
+// occ != null: no launch; *occ = the instance's resident wavefronts per CU (one-wavefront
+// workgroups with `lds` bytes of LDS each)
 template <int TR, int CR, int QMAX, int PB>
-static hipError_t launch_one(const SearchParams& p, dim3 grid, dim3 block, size_t lds, hipStream_t s) {
+static hipError_t launch_one(const SearchParams& p, dim3 grid, dim3 block, size_t lds, hipStream_t s, int* occ) {
     auto k = search_kernel<TR, CR, QMAX, BS_INST_MODE, PB>;
+    if (occ) return hipOccupancyMaxActiveBlocksPerMultiprocessor(occ, k, 64, lds);
     if (lds > 65536) {
         hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(k),
                                            hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
@@ -22,61 +25,62 @@ static hipError_t launch_one(const SearchParams& p, dim3 grid, dim3 block, size_
 }
 
 template <int TR, int CR>
-static hipError_t launch_p(const SearchParams& p, int PB, dim3 g, dim3 b, size_t lds, hipStream_t s) {
+static hipError_t launch_p(const SearchParams& p, int PB, dim3 g, dim3 b, size_t lds, hipStream_t s, int* occ) {
     // every dim <= 1024 fits 4 float4 chunks per lane (bsd::l2_shape).  Narrow RaBitQ codes
     // mean dim <= 128, hence PB = 2; wide codes mean dim > 128, hence PB >= 4.
     if constexpr (BS_INST_MODE == 2) {
         (void)PB;
-        return launch_one<TR, CR, 4, 2>(p, g, b, lds, s);
+        return launch_one<TR, CR, 4, 2>(p, g, b, lds, s, occ);
     } else if constexpr (BS_INST_MODE == 3) {
-        return PB == 4 ? launch_one<TR, CR, 4, 4>(p, g, b, lds, s) : launch_one<TR, CR, 4, 8>(p, g, b, lds, s);
+        return PB == 4 ? launch_one<TR, CR, 4, 4>(p, g, b, lds, s, occ) : launch_one<TR, CR, 4, 8>(p, g, b, lds, s, occ);
     } else {
         switch (PB) {
-        case 2: return launch_one<TR, CR, 4, 2>(p, g, b, lds, s);
-        case 4: return launch_one<TR, CR, 4, 4>(p, g, b, lds, s);
-        default: return launch_one<TR, CR, 4, 8>(p, g, b, lds, s);
+        case 2: return launch_one<TR, CR, 4, 2>(p, g, b, lds, s, occ);
+        case 4: return launch_one<TR, CR, 4, 4>(p, g, b, lds, s, occ);
+        default: return launch_one<TR, CR, 4, 8>(p, g, b, lds, s, occ);
         }
     }
 }
 
 template <int TR>
-static hipError_t launch_c(const SearchParams& p, int CR, int PB, dim3 g, dim3 b, size_t lds, hipStream_t s) {
-    return CR == 1 ? launch_p<TR, 1>(p, PB, g, b, lds, s) : launch_p<TR, 2>(p, PB, g, b, lds, s);
+static hipError_t launch_c(const SearchParams& p, int CR, int PB, dim3 g, dim3 b, size_t lds, hipStream_t s,
+                           int* occ) {
+    return CR == 1 ? launch_p<TR, 1>(p, PB, g, b, lds, s, occ) : launch_p<TR, 2>(p, PB, g, b, lds, s, occ);
 }
 
 static hipError_t launch_any(const SearchParams& p, int TR, int CR, int PB, dim3 g, dim3 b, size_t lds,
-                             hipStream_t s) {
+                             hipStream_t s, int* occ) {
     switch (TR) {
-    case 1: return launch_c<1>(p, CR, PB, g, b, lds, s);
-    case 2: return launch_c<2>(p, CR, PB, g, b, lds, s);
-    case 4: return launch_c<4>(p, CR, PB, g, b, lds, s);
-    case 8: return launch_c<8>(p, CR, PB, g, b, lds, s);
+    case 1: return launch_c<1>(p, CR, PB, g, b, lds, s, occ);
+    case 2: return launch_c<2>(p, CR, PB, g, b, lds, s, occ);
+    case 4: return launch_c<4>(p, CR, PB, g, b, lds, s, occ);
+    case 8: return launch_c<8>(p, CR, PB, g, b, lds, s, occ);
 #if BS_INST_MODE >= 2
-    case 12: return launch_c<12>(p, CR, PB, g, b, lds, s);  // rabitq beams of 513..768
+    case 12: return launch_c<12>(p, CR, PB, g, b, lds, s, occ);  // rabitq beams of 513..768
 #endif
-    default: return launch_c<16>(p, CR, PB, g, b, lds, s);
+    default: return launch_c<16>(p, CR, PB, g, b, lds, s, occ);
     }
 }
 
 #if BS_INST_MODE == 0
 hipError_t launch_search_hash(const SearchParams& p, int TR, int CR, int PB, dim3 g, dim3 b, size_t lds,
-                              hipStream_t s) {
-    return launch_any(p, TR, CR, PB, g, b, lds, s);
+                              hipStream_t s, int* occ) {
+    return launch_any(p, TR, CR, PB, g, b, lds, s, occ);
 }
 #elif BS_INST_MODE == 1
 hipError_t launch_search_bloom(const SearchParams& p, int TR, int CR, int PB, dim3 g, dim3 b, size_t lds,
-                               hipStream_t s) {
-    return launch_any(p, TR, CR, PB, g, b, lds, s);
+                              hipStream_t s, int* occ) {
+    return launch_any(p, TR, CR, PB, g, b, lds, s, occ);
 }
 #elif BS_INST_MODE == 2
 hipError_t launch_search_rabitq(const SearchParams& p, int TR, int CR, int PB, dim3 g, dim3 b, size_t lds,
-                                hipStream_t s) {
-    return launch_any(p, TR, CR, PB, g, b, lds, s);
+                              hipStream_t s, int* occ) {
+    return launch_any(p, TR, CR, PB, g, b, lds, s, occ);
 }
 #else
 hipError_t launch_search_rabitq_wide(const SearchParams& p, int TR, int CR, int PB, dim3 g, dim3 b, size_t lds,
-                                     hipStream_t s) {
-    return launch_any(p, TR, CR, PB, g, b, lds, s);
+                              hipStream_t s, int* occ) {
+    return launch_any(p, TR, CR, PB, g, b, lds, s, occ);
 }
 #endif
 

@@ -104,11 +104,12 @@ def test_group_modes_identical_and_deterministic(gpu):
             assert np.array_equal(ids, ref), m
 
 
-@pytest.mark.parametrize("nq", [700, 1500, 3000])
+@pytest.mark.parametrize("nq", [700, 1100, 1500, 2500, 3000])
 def test_base_waves_per_query(gpu, nq):
     """base mode gives a query 4, 2 or 1 wavefronts depending on how many queries the launch
-    has (nq * 4 <= 16 * CUs, nq * 2 <= 16 * CUs, else 1 on a 256-CU MI355X): the split of a
-    candidate batch over wavefronts must not change any result or counter"""
+    has (against 16 wavefronts per CU, or the instance's occupancy for beams of 256 and
+    more; on a 256-CU MI355X these nq cover all three splits): the split of a candidate batch
+    over wavefronts must not change any result or counter"""
     ds = dataset(3000, 64, 32, nq)
     for topk in (64, 256):
         assert_same(*run_both(ds, "base", 10, topk), f"base nq={nq} topk={topk}")
