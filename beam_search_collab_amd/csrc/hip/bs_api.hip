@@ -71,6 +71,9 @@ struct bs_index_s {
     float* d_pnorm = nullptr;
     uint32_t* d_ows = nullptr;  // key[ORDER_CHUNK] | qmap[ORDER_CHUNK] | hist[P] | cursor[P]
     hipEvent_t ws_free = nullptr;
+    // device staging of bs_search (host buffers): grows to the largest call, reused after
+    void* d_stage = nullptr;
+    size_t stage_bytes = 0;
 };
 
 namespace {
@@ -341,6 +344,7 @@ extern "C" void bs_index_destroy(bs_index ix) {
     if (ix->d_pivT) (void)hipFree(ix->d_pivT);
     if (ix->d_pnorm) (void)hipFree(ix->d_pnorm);
     if (ix->d_ows) (void)hipFree(ix->d_ows);
+    if (ix->d_stage) (void)hipFree(ix->d_stage);
     delete ix;
 }
 
@@ -596,27 +600,28 @@ extern "C" int bs_search(bs_index ix, const bs_search_cfg* cfg, const float* que
         return BS_OK;
     }
     if (!queries || !results) return fail(BS_EINVAL, "queries and results must be given");
-    float* dq = nullptr;
-    uint32_t* dr = nullptr;
-    float* dd = nullptr;
-    uint32_t* dp = nullptr;
-    auto cleanup = [&]() {
-        if (dq) (void)hipFree(dq);
-        if (dr) (void)hipFree(dr);
-        if (dd) (void)hipFree(dd);
-        if (dp) (void)hipFree(dp);
-    };
-    const size_t qb = nq * ix->dim * sizeof(float), rb = nq * cfg->K * sizeof(uint32_t);
-    if (hipMalloc(&dq, qb) != hipSuccess || hipMalloc(&dr, rb) != hipSuccess ||
-        (dists && hipMalloc(&dd, rb) != hipSuccess) || hipMalloc(&dp, nq * 5 * 4) != hipSuccess) {
-        cleanup();
-        return fail(BS_ENOMEM, "hipMalloc of the query buffers failed");
+    // queries | results | dists | per-query counters, each 256-B aligned, in the index's
+    // staging buffer (calls on one index are serialised and this one is synchronous)
+    auto al = [](size_t v) { return (v + 255) & ~static_cast<size_t>(255); };
+    const size_t qb = nq * ix->dim * sizeof(float), rb = nq * cfg->K * sizeof(uint32_t), pb = nq * 5 * 4;
+    const size_t need = al(qb) + al(rb) + (dists ? al(rb) : 0) + al(pb);
+    if (need > ix->stage_bytes) {
+        if (ix->d_stage) (void)hipFree(ix->d_stage);
+        ix->d_stage = nullptr;
+        ix->stage_bytes = 0;
+        if (hipMalloc(&ix->d_stage, need) != hipSuccess) {
+            ix->d_stage = nullptr;
+            return fail(BS_ENOMEM, "hipMalloc of the query staging buffer failed");
+        }
+        ix->stage_bytes = need;
     }
+    char* base = static_cast<char*>(ix->d_stage);
+    float* dq = reinterpret_cast<float*>(base);
+    uint32_t* dr = reinterpret_cast<uint32_t*>(base + al(qb));
+    float* dd = dists ? reinterpret_cast<float*>(base + al(qb) + al(rb)) : nullptr;
+    uint32_t* dp = reinterpret_cast<uint32_t*>(base + al(qb) + al(rb) + (dists ? al(rb) : 0));
     hipError_t e = hipMemcpy(dq, queries, qb, hipMemcpyHostToDevice);
-    if (e != hipSuccess) {
-        cleanup();
-        return fail(BS_EHIP, std::string("query upload failed: ") + hipGetErrorString(e));
-    }
+    if (e != hipSuccess) return fail(BS_EHIP, std::string("query upload failed: ") + hipGetErrorString(e));
     bs_stats st;
     rc = bs_search_device(ix, cfg, dq, nq, dr, dd, dp, nullptr, 1, &st);
     if (rc == BS_OK) {
@@ -624,7 +629,6 @@ extern "C" int bs_search(bs_index ix, const bs_search_cfg* cfg, const float* que
         if (e == hipSuccess && dists) e = hipMemcpy(dists, dd, rb, hipMemcpyDeviceToHost);
         if (e != hipSuccess) rc = fail(BS_EHIP, std::string("result download failed: ") + hipGetErrorString(e));
     }
-    cleanup();
     if (rc == BS_OK && stats) *stats = st;
     return rc;
 } catch (...) {

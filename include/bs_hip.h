@@ -91,7 +91,9 @@ int bs_index_attach_rabitq(bs_index idx, const uint32_t* codes, const float* fac
 /* Search nq host-resident queries (nq*dim f32); results (host, nq*K u32) and optional
  * dists (host, nq*K f32, NULL allowed) are written.  Replaces one timed launch of
  * run_base / run_warp / run_rabitq (src/gpu_cli.cu:140-349) including the query upload
- * and result download of gpu_cli main (src/gpu_cli.cu:399-421,481). stats nullable. */
+ * and result download of gpu_cli main (src/gpu_cli.cu:399-421,481). stats nullable.
+ * The device staging buffers belong to the index: they grow to the largest call and are
+ * reused (freed by bs_index_destroy). */
 int bs_search(bs_index idx, const bs_search_cfg* cfg, const float* queries, uint64_t nq,
               uint32_t* results, float* dists, bs_stats* stats);
 
