@@ -143,6 +143,40 @@ def test_query_order_changes_no_result(gpu, nq):
         g.set_query_order(1)
 
 
+def test_query_order_chunked_launches(gpu):
+    """more than 262144 queries run as several scheduled launches (the workspace's size):
+    every query still gets the result of the unscheduled launch"""
+    ds = dataset(3000, 64, 32, 64)
+    g = ds["g"]
+    rng = np.random.default_rng(9)
+    q = np.repeat(ds["q"], 4100, axis=0)[: 262144 + 777]
+    q = q + rng.standard_normal(q.shape).astype(np.float32)  # distinct queries
+    cfg = GPUBaseSearchCfg(64, 1024, ds["entry"], 1024, 16)
+    try:
+        g.set_query_order(0)
+        want, _, s0 = g.search(q, 10, "warp2", cfg)
+        g.set_query_order(1)
+        got, _, s1 = g.search(q, 10, "warp2", cfg)
+    finally:
+        g.set_query_order(1)
+    assert np.array_equal(got, want)
+    assert s0["expansions"] == s1["expansions"] and s0["dist_evals"] == s1["dist_evals"]
+
+
+def test_host_buffer_calls_of_changing_size(gpu):
+    """bs_search keeps its device staging between calls: calls that grow and shrink the batch
+    (with and without distances) give the results of the device-buffer path"""
+    ds = dataset(3000, 64, 32, 300)
+    g, q = ds["g"], ds["q"]
+    cfg = GPUBaseSearchCfg(64, 1024, ds["entry"], 1024, 16)
+    ref, dref, _ = g.search(q, 10, "base", cfg, with_dists=True)
+    for rows, dists in ((5, False), (300, True), (17, True), (300, False), (1, True)):
+        ids, d, _ = g.search(q[:rows], 10, "base", cfg, with_dists=dists)
+        assert np.array_equal(ids, ref[:rows]), rows
+        if dists:
+            assert d.tobytes() == dref[:rows].tobytes(), rows
+
+
 def test_k_equals_topk_and_empty_results(gpu):
     # tiny graph: fewer reachable nodes than K -> trailing 0xFFFFFFFF
     base = host.gen_normalized(40, 16, 3)
