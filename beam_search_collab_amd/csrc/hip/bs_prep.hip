@@ -33,67 +33,185 @@ namespace bsp {
 
 using namespace bsw;
 
-constexpr uint32_t EP_ROWS = 256;    // rows per LDS chunk (64 columns each: 64 KB)
-constexpr uint32_t EP_THREADS = 1024;
+constexpr uint32_t EP_COLS = 16;                        // dimensions per workgroup
+constexpr uint32_t EP_ROWS = 1024;                      // rows per LDS chunk
+constexpr uint32_t EP_S = EP_ROWS + 4;                  // floats per column of a chunk (see entry_centroid)
+constexpr uint32_t EP_THREADS = 1024;                   // wavefront 0 adds, the other 15 stage rows
+constexpr uint32_t EP_STAGERS = EP_THREADS / 64 - 1;
+constexpr uint32_t EP_GROUPS = EP_ROWS / 16;            // 16-row groups per chunk
+constexpr uint32_t EP_GPW = (EP_GROUPS + EP_STAGERS - 1) / EP_STAGERS;  // groups per staging wavefront
+constexpr size_t EP_LDS = (2 * EP_COLS * EP_S + 32) * sizeof(float);  // two chunks + 32 spare: 128.6 KB
 
 __device__ __forceinline__ uint32_t orderable(float f) {
     const uint32_t b = __float_as_uint(f);
     return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
 }
 
+// LDS reads issued outside the compiler's view, for a software pipeline it would otherwise
+// restructure.  The compiler does not count them, so every result is claimed through
+// lgkm_wait (at most N LDS operations of this wavefront still outstanding, the register
+// tied to the wait so no use moves above it) or lgkm_drain before it is read or its
+// registers are reused.  Only the wavefront's own LDS operations count: LDS returns in
+// issue order, so waiting down to N completes all but the N most recent.
+__device__ __forceinline__ uint32_t lds_address(const float* p) {
+    return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((const __attribute__((address_space(3))) float*)p));
+}
+using f32x4 = float __attribute__((ext_vector_type(4)));
+template <int OFF>
+__device__ __forceinline__ void lds_read_b128(f32x4& v, uint32_t addr) {
+    asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "n"(OFF) : "memory");
+}
+template <int N>
+__device__ __forceinline__ void lgkm_wait(f32x4& a, f32x4& b, f32x4& c, f32x4& d) {
+    asm volatile("s_waitcnt lgkmcnt(%4)" : "+v"(a), "+v"(b), "+v"(c), "+v"(d) : "n"(N) : "memory");
+}
+__device__ __forceinline__ void lgkm_drain(f32x4 (&w)[8]) {
+    asm volatile("s_waitcnt lgkmcnt(0)"
+                 : "+v"(w[0]), "+v"(w[1]), "+v"(w[2]), "+v"(w[3]), "+v"(w[4]), "+v"(w[5]), "+v"(w[6]), "+v"(w[7])
+                 :
+                 : "memory");
+}
+
 // The centroid is one dependent chain of n additions per dimension, so the only
-// parallelism is across dimensions: workgroup x owns dimensions [64x, 64x + 64), its
-// first wavefront adds (lane = dimension) while the other 15 wavefronts stream the next
-// chunk of rows into the other half of a double buffer in LDS.
+// parallelism is across dimensions, and a wavefront's chain costs the same whatever the
+// number of its lanes that take part (about 6 cycles per dependent v_add).  Workgroup x
+// owns the 16 dimensions [16x, 16x + 16) (so a 128-dimensional set keeps 8 CUs busy and
+// each CU needs only 64 bytes per row); its first wavefront adds (dimension = lane % 16),
+// one v_add per row and one ds_read_b128 per four rows, while the other 15 wavefronts keep
+// it fed.  Chunks of EP_ROWS rows are stored column-major in LDS (a column's rows
+// contiguous, columns EP_S floats apart, so 16 lanes hit 16 distinct 4-bank groups), two chunks in LDS and two
+// more in flight in the stagers' registers: loads are issued two chunks ahead, so their
+// latency overlaps two chunks of additions.  A stager lane (r, k) = (lane / 16, lane % 16)
+// loads rows 4r..4r+3 of a 16-row group in column k, one row per load instruction (a
+// wavefront instruction covers 4 rows x 64 bytes), and stores them with one ds_write_b128.
+// In float mode the stagers form the products row[d] * inv, so the chain is additions only.
 //   float:  c += row[d] * inv                       (compute_entry_point)
 //   double: c += (double)row[d], then c / n         (find_medoid)
 template <typename T>
 __global__ void __launch_bounds__(EP_THREADS) entry_centroid(const float* vecs, uint64_t n, uint32_t dim,
                                                             uint32_t dstride, float inv, T* cent,
                                                             unsigned long long* best) {
-    extern __shared__ float buf[];  // [2][EP_ROWS][64]
+    extern __shared__ __attribute__((aligned(16))) float buf[];  // [2][EP_COLS][EP_S], 32 spare
     const uint32_t lane = lane_id(), wave = uniform(threadIdx.x >> 6);
-    const uint32_t col0 = blockIdx.x * 64;
+    const uint32_t k = lane & (EP_COLS - 1), rq = lane / EP_COLS;
+    const uint32_t col = blockIdx.x * EP_COLS + k;
     const uint64_t nchunk = (n + EP_ROWS - 1) / EP_ROWS;
     if (blockIdx.x == 0 && threadIdx.x == 0) {
         // float: the key (FLT_MAX, row 0); double: the distance bits of DBL_MAX
         if constexpr (sizeof(T) == 4) *best = static_cast<unsigned long long>(orderable(FLT_MAX)) << 32;
         else *best = static_cast<unsigned long long>(__double_as_longlong(DBL_MAX));
     }
-    // stage chunk c into buffer half h with threads [t0, EP_THREADS)
-    auto stage = [&](uint64_t c, uint32_t h, uint32_t t0) __attribute__((always_inline)) {
-        float* dst = buf + h * (EP_ROWS * 64);
-        const uint64_t r0 = c * EP_ROWS;
-        for (uint32_t e = threadIdx.x - t0; e < EP_ROWS * 64; e += EP_THREADS - t0) {
-            const uint32_t r = e >> 6, k = e & 63u;
-            const uint64_t row = r0 + r;
-            float v = 0.0f;
-            if (row < n && col0 + k < dim) v = vecs[row * dstride + col0 + k];
-            dst[e] = v;
+    // stager wavefront w (1..15) owns the 16-row groups g = (w - 1) + 15 j of every chunk
+    const uint32_t sw = wave - 1;
+    float ra[EP_GPW * 4], rb[EP_GPW * 4];
+    // Every load is issued unconditionally (a fixed number per chunk, so the compiler waits
+    // for exactly the older chunk), with rows past n clamped to n - 1 and columns past dim to
+    // dim - 1: the adding wavefront never reads those rows nor writes those columns.
+    const uint32_t coff = (col < dim ? col : dim - 1) * 4u;
+    const uint32_t rowbytes = dstride * 4u;  // dstride <= 1024: a chunk spans at most 4 MB
+    auto load = [&](uint64_t c, float (&r)[EP_GPW * 4]) __attribute__((always_inline)) {
+        const uint64_t row0 = std::min<uint64_t>(c * EP_ROWS, n - 1);
+        const uint32_t last = static_cast<uint32_t>(std::min<uint64_t>(n - 1 - row0, EP_ROWS - 1));
+        const char* base = reinterpret_cast<const char*>(vecs + row0 * dstride) + coff;
+#pragma unroll
+        for (uint32_t j = 0; j < EP_GPW; ++j) {
+            const uint32_t g = sw + j * EP_STAGERS;
+#pragma unroll
+            for (uint32_t t = 0; t < 4; ++t) {
+                const uint32_t rr = std::min(16 * g + 4 * rq + t, last);
+                r[4 * j + t] = *reinterpret_cast<const float*>(base + static_cast<uint64_t>(rr) * rowbytes);
+            }
         }
     };
-    stage(0, 0, 0);
-    __syncthreads();
-    T s = 0;
-    for (uint64_t c = 0; c < nchunk; ++c) {
-        const uint32_t h = static_cast<uint32_t>(c & 1);
-        if (wave == 0) {
-            const float* src = buf + h * (EP_ROWS * 64) + lane;
-            const uint32_t rows = static_cast<uint32_t>(n - c * EP_ROWS < EP_ROWS ? n - c * EP_ROWS : EP_ROWS);
-            if constexpr (sizeof(T) == 4) {
-#pragma unroll 16
-                for (uint32_t r = 0; r < rows; ++r) s = s + src[r * 64] * inv;
-            } else {
-#pragma unroll 16
-                for (uint32_t r = 0; r < rows; ++r) s = s + static_cast<double>(src[r * 64]);
+    auto store = [&](uint32_t h, const float (&r)[EP_GPW * 4]) __attribute__((always_inline)) {
+        float* dst = buf + (h * EP_COLS + k) * EP_S + 4 * rq;
+#pragma unroll
+        for (uint32_t j = 0; j < EP_GPW; ++j) {
+            const uint32_t g = sw + j * EP_STAGERS;
+            if (g < EP_GROUPS) {
+                float4 v = make_float4(r[4 * j], r[4 * j + 1], r[4 * j + 2], r[4 * j + 3]);
+                if constexpr (sizeof(T) == 4) v = make_float4(v.x * inv, v.y * inv, v.z * inv, v.w * inv);
+                *reinterpret_cast<float4*>(dst + 16 * g) = v;
             }
-        } else if (c + 1 < nchunk) {
-            stage(c + 1, h ^ 1u, 64);
+        }
+    };
+    T s = 0;
+    // The adding wavefront keeps eight ds_read_b128 (32 rows) in flight: each half block
+    // of 16 rows is added, then its registers take the 16 rows 32 rows further on.  All 64 lanes
+    // run the chain (lanes 16-63 repeat lanes 0-15: a partly masked wavefront adds slower).  The compiler turns such a
+    // rotation of plain loads back into load-then-use blocks (one LDS latency per 32 rows),
+    // so the reads are issued by lds_read_b128 and waited for by lgkm_wait; the reads of
+    // the last block run past the column's rows into the next column or the 32 spare floats
+    // at the end of the buffer, and are drained, never added.
+    auto consume = [&](uint64_t c, uint32_t h) __attribute__((always_inline)) {
+        const float* src = buf + (h * EP_COLS + k) * EP_S;
+        const uint32_t rows = static_cast<uint32_t>(n - c * EP_ROWS < EP_ROWS ? n - c * EP_ROWS : EP_ROWS);
+        const uint32_t nblk = rows / 32;
+        uint32_t addr = lds_address(src);
+        f32x4 w[8];
+        lds_read_b128<0>(w[0], addr);
+        lds_read_b128<16>(w[1], addr);
+        lds_read_b128<32>(w[2], addr);
+        lds_read_b128<48>(w[3], addr);
+        lds_read_b128<64>(w[4], addr);
+        lds_read_b128<80>(w[5], addr);
+        lds_read_b128<96>(w[6], addr);
+        lds_read_b128<112>(w[7], addr);
+        for (uint32_t b = 0; b < nblk; ++b) {
+            addr += 128;
+#define BSP_ADD(v)                                  \
+    s = s + static_cast<T>(v.x);                    \
+    s = s + static_cast<T>(v.y);                    \
+    s = s + static_cast<T>(v.z);                    \
+    s = s + static_cast<T>(v.w);
+            lgkm_wait<4>(w[0], w[1], w[2], w[3]);
+            BSP_ADD(w[0]) BSP_ADD(w[1]) BSP_ADD(w[2]) BSP_ADD(w[3])
+            lds_read_b128<0>(w[0], addr);
+            lds_read_b128<16>(w[1], addr);
+            lds_read_b128<32>(w[2], addr);
+            lds_read_b128<48>(w[3], addr);
+            lgkm_wait<4>(w[4], w[5], w[6], w[7]);
+            BSP_ADD(w[4]) BSP_ADD(w[5]) BSP_ADD(w[6]) BSP_ADD(w[7])
+            lds_read_b128<64>(w[4], addr);
+            lds_read_b128<80>(w[5], addr);
+            lds_read_b128<96>(w[6], addr);
+            lds_read_b128<112>(w[7], addr);
+#undef BSP_ADD
+        }
+        lgkm_drain(w);
+        for (uint32_t r = 32 * nblk; r < rows; ++r) s = s + static_cast<T>(src[r]);
+    };
+    // prologue: chunk 0 into LDS half 0, chunk 1 held in rb, chunk 2 in flight into ra
+    if (wave != 0) {
+        load(0, ra);
+        load(1, rb);
+        store(0, ra);
+        load(2, ra);
+    }
+    __syncthreads();
+    // chunk c is in LDS half c & 1; while it is added, the stagers store chunk c + 1 into
+    // the other half and issue the loads of chunk c + 3 into the registers they freed
+    // (past the last chunk the stagers go on storing into the half that is not being read
+    // and loading clamped rows; nothing reads them)
+    for (uint64_t c = 0; c < nchunk; c += 2) {
+        if (wave == 0) {
+            consume(c, 0);
+        } else {
+            store(1, rb);
+            load(c + 3, rb);
+        }
+        __syncthreads();
+        if (c + 1 >= nchunk) break;
+        if (wave == 0) {
+            consume(c + 1, 1);
+        } else {
+            store(0, ra);
+            load(c + 4, ra);
         }
         __syncthreads();
     }
     if constexpr (sizeof(T) == 8) s = s / static_cast<double>(n);
-    if (wave == 0 && col0 + lane < dim) cent[col0 + lane] = s;
+    if (wave == 0 && lane < EP_COLS && col < dim) cent[col] = s;
 }
 
 // Thread per row: its float distance in dimension order, then the least (dist, row) of
@@ -275,11 +393,11 @@ extern "C" int bs_index_entry_point(bs_index idx, uint32_t* entry) try {
         return pfail(BS_ENOMEM, "hipMalloc of the entry-point buffers failed");
     }
     const float inv = 1.0f / static_cast<float>(n);
-    const size_t lds = 2 * bsp::EP_ROWS * 64 * sizeof(float);
+    const size_t lds = bsp::EP_LDS;
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(bsp::entry_centroid<float>),
                                        hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
     if (e == hipSuccess) {
-        hipLaunchKernelGGL(bsp::entry_centroid<float>, dim3((dim + 63) / 64), dim3(bsp::EP_THREADS), lds, nullptr, vecs, n,
+        hipLaunchKernelGGL(bsp::entry_centroid<float>, dim3((dim + bsp::EP_COLS - 1) / bsp::EP_COLS), dim3(bsp::EP_THREADS), lds, nullptr, vecs, n,
                            dim, dstride, inv, cent, best);
         e = hipGetLastError();
     }
@@ -358,12 +476,12 @@ extern "C" int bs_index_build_rabitq(bs_index idx, uint32_t seed, uint32_t* code
     hipError_t e = hipMemcpy(d_signs, signs_out, pdim * sizeof(float), hipMemcpyHostToDevice);
     if (e == hipSuccess) e = hipMemcpy(d_index, &init_index, sizeof(init_index), hipMemcpyHostToDevice);
     // medoid (find_medoid, build_rabitq.cpp:59-99) in double
-    const size_t lds = 2 * bsp::EP_ROWS * 64 * sizeof(float);
+    const size_t lds = bsp::EP_LDS;
     if (e == hipSuccess)
         e = hipFuncSetAttribute(reinterpret_cast<const void*>(bsp::entry_centroid<double>),
                                 hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
     if (e == hipSuccess) {
-        hipLaunchKernelGGL(bsp::entry_centroid<double>, dim3((dim + 63) / 64), dim3(bsp::EP_THREADS), lds, nullptr,
+        hipLaunchKernelGGL(bsp::entry_centroid<double>, dim3((dim + bsp::EP_COLS - 1) / bsp::EP_COLS), dim3(bsp::EP_THREADS), lds, nullptr,
                            vecs, n, dim, dstride, 0.0f, d_cent, d_best);
         e = hipGetLastError();
     }
