@@ -214,66 +214,74 @@ __global__ void __launch_bounds__(EP_THREADS) entry_centroid(const float* vecs, 
     if (wave == 0 && lane < EP_COLS && col < dim) cent[col] = s;
 }
 
-// Thread per row: its float distance in dimension order, then the least (dist, row) of
-// the rows with dist < FLT_MAX by one 64-bit atomic minimum per wavefront.
-__global__ void __launch_bounds__(256) entry_nearest(const float* vecs, uint64_t n, uint32_t dim,
-                                                     uint32_t dstride, const float* cent,
-                                                     unsigned long long* best) {
-    __shared__ float c[1024];
-    for (uint32_t k = threadIdx.x; k < dim; k += 256) c[k] = cent[k];
-    __syncthreads();
-    const uint64_t i = static_cast<uint64_t>(blockIdx.x) * 256 + threadIdx.x;
-    unsigned long long key = ~0ull;
-    if (i < n) {
-        const float4* row = reinterpret_cast<const float4*>(vecs + i * dstride);
-        float s = 0.0f;
-        uint32_t k = 0;
-        for (; k + 4 <= dim; k += 4) {
-            const float4 v = row[k >> 2];
-            float d = v.x - c[k];
-            s = s + d * d;
-            d = v.y - c[k + 1];
-            s = s + d * d;
-            d = v.z - c[k + 2];
-            s = s + d * d;
-            d = v.w - c[k + 3];
-            s = s + d * d;
-        }
-        for (; k < dim; ++k) {
-            const float d = vecs[i * dstride + k] - c[k];
-            s = s + d * d;
-        }
-        if (s < FLT_MAX) key = (static_cast<unsigned long long>(orderable(s)) << 32) | i;
-    }
-    unsigned long long t;
-    t = xor_lane64<1>(key); key = t < key ? t : key;
-    t = xor_lane64<2>(key); key = t < key ? t : key;
-    t = xor_lane64<4>(key); key = t < key ? t : key;
-    t = xor_lane64<8>(key); key = t < key ? t : key;
-    t = xor_lane64<16>(key); key = t < key ? t : key;
-    t = xor_lane64<32>(key); key = t < key ? t : key;
-    if (lane_id() == 0 && key != ~0ull) atomicMin(best, key);
-}
+// Distance of every row to the centroid in dimension order, as the reference's loops form it
+// (float: diff = row[d] - c[d], dist += diff * diff; double: the same with row[d] widened).
+// A wavefront owns 64 rows, a lane one row's dependent chain of dim steps.  Its rows pass
+// through a wavefront-private LDS tile of 64 rows x 64 dimensions: loaded coalesced (16
+// lanes per row, a float4 each, 4 rows per load instruction, every tile's loads in flight
+// together), stored row-major with rows EP_TS floats apart (16 lanes of a b128 phase hit 16
+// distinct 4-bank groups), then each lane reads its own row back one float4 at a time.
+//   float:  the least (orderable dist, row) with dist < FLT_MAX by a 64-bit atomic minimum
+//   double: every row's dist, and the least distance bits (non-negative doubles order as
+//           their bit patterns); medoid_index then takes the least row at that distance
+constexpr uint32_t EP_TS = 64 + 4;
+constexpr size_t ND_LDS = 4 * 64 * EP_TS * sizeof(float);  // four wavefronts' tiles
 
-// find_medoid's nearest row in double: pass 1 stores every row's distance and the least
-// distance bits (non-negative doubles order as their bit patterns), pass 2 the least row
-// index at that distance.
-__global__ void __launch_bounds__(256) medoid_dist(const float* vecs, uint64_t n, uint32_t dim, uint32_t dstride,
-                                                   const double* cent, double* dist, unsigned long long* best) {
-    __shared__ double c[1024];
+template <typename T>
+__global__ void __launch_bounds__(256) row_dist(const float* vecs, uint64_t n, uint32_t dim, uint32_t dstride,
+                                                const T* cent, T* dist, unsigned long long* best) {
+    __shared__ T c[1024];
+    extern __shared__ __attribute__((aligned(16))) float tiles[];
     for (uint32_t k = threadIdx.x; k < dim; k += 256) c[k] = cent[k];
     __syncthreads();
-    const uint64_t i = static_cast<uint64_t>(blockIdx.x) * 256 + threadIdx.x;
+    const uint32_t lane = lane_id(), wave = uniform(threadIdx.x >> 6);
+    const uint64_t r0 = (static_cast<uint64_t>(blockIdx.x) * 4 + wave) * 64;
+    if (r0 >= n) return;  // wavefront-uniform: no barrier follows
+    float* tile = tiles + wave * 64 * EP_TS;
+    // loader role: row r0 + 4 i + lane / 16 (clamped to n - 1), columns 4 (lane % 16) + 0..3
+    const uint32_t lr = lane >> 4, lc = (lane & 15u) * 4;
+    const uint64_t i = r0 + lane;
+    T s = 0;
+    for (uint32_t d0 = 0; d0 < dim; d0 += 64) {
+        f32x4 v[16];
+#pragma unroll
+        for (uint32_t t = 0; t < 16; ++t) {
+            const uint64_t row = std::min<uint64_t>(r0 + 4 * t + lr, n - 1);
+            // columns at or past dim are never added; they read column 0 of the row
+            const uint32_t cc = d0 + lc < dim ? d0 + lc : 0u;
+            v[t] = *reinterpret_cast<const f32x4*>(vecs + row * dstride + cc);
+        }
+        wave_sync();  // the previous tile's reads are done before it is overwritten
+#pragma unroll
+        for (uint32_t t = 0; t < 16; ++t) *reinterpret_cast<f32x4*>(tile + (4 * t + lr) * EP_TS + lc) = v[t];
+        wave_sync();
+        const float* mine = tile + lane * EP_TS;
+        const uint32_t cols = dim - d0 < 64 ? dim - d0 : 64;
+        uint32_t k = 0;
+        for (; k + 4 <= cols; k += 4) {
+            const f32x4 x = *reinterpret_cast<const f32x4*>(mine + k);
+            T e = static_cast<T>(x.x) - c[d0 + k];
+            s = s + e * e;
+            e = static_cast<T>(x.y) - c[d0 + k + 1];
+            s = s + e * e;
+            e = static_cast<T>(x.z) - c[d0 + k + 2];
+            s = s + e * e;
+            e = static_cast<T>(x.w) - c[d0 + k + 3];
+            s = s + e * e;
+        }
+        for (; k < cols; ++k) {
+            const T e = static_cast<T>(mine[k]) - c[d0 + k];
+            s = s + e * e;
+        }
+    }
     unsigned long long key = ~0ull;
     if (i < n) {
-        const float* row = vecs + i * dstride;
-        double s = 0.0;
-        for (uint32_t k = 0; k < dim; ++k) {
-            const double d = static_cast<double>(row[k]) - c[k];
-            s = s + d * d;
+        if constexpr (sizeof(T) == 4) {
+            if (s < FLT_MAX) key = (static_cast<unsigned long long>(orderable(s)) << 32) | i;
+        } else {
+            dist[i] = s;
+            if (s < DBL_MAX) key = static_cast<unsigned long long>(__double_as_longlong(s));
         }
-        dist[i] = s;
-        if (s < DBL_MAX) key = static_cast<unsigned long long>(__double_as_longlong(s));
     }
     unsigned long long t;
     t = xor_lane64<1>(key); key = t < key ? t : key;
@@ -282,7 +290,7 @@ __global__ void __launch_bounds__(256) medoid_dist(const float* vecs, uint64_t n
     t = xor_lane64<8>(key); key = t < key ? t : key;
     t = xor_lane64<16>(key); key = t < key ? t : key;
     t = xor_lane64<32>(key); key = t < key ? t : key;
-    if (lane_id() == 0 && key != ~0ull) atomicMin(best, key);
+    if (lane == 0 && key != ~0ull) atomicMin(best, key);
 }
 
 __global__ void __launch_bounds__(256) medoid_index(uint64_t n, const double* dist, const unsigned long long* best,
@@ -401,9 +409,12 @@ extern "C" int bs_index_entry_point(bs_index idx, uint32_t* entry) try {
                            dim, dstride, inv, cent, best);
         e = hipGetLastError();
     }
+    if (e == hipSuccess)
+        e = hipFuncSetAttribute(reinterpret_cast<const void*>(bsp::row_dist<float>),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(bsp::ND_LDS));
     if (e == hipSuccess) {
-        hipLaunchKernelGGL(bsp::entry_nearest, dim3(static_cast<uint32_t>((n + 255) / 256)), dim3(256), 0, nullptr,
-                           vecs, n, dim, dstride, cent, best);
+        hipLaunchKernelGGL(bsp::row_dist<float>, dim3(static_cast<uint32_t>((n + 255) / 256)), dim3(256), bsp::ND_LDS,
+                           nullptr, vecs, n, dim, dstride, cent, nullptr, best);
         e = hipGetLastError();
     }
     unsigned long long key = 0;
@@ -486,9 +497,12 @@ extern "C" int bs_index_build_rabitq(bs_index idx, uint32_t seed, uint32_t* code
         e = hipGetLastError();
     }
     const dim3 rows_grid(static_cast<uint32_t>((n + 255) / 256));
+    if (e == hipSuccess)
+        e = hipFuncSetAttribute(reinterpret_cast<const void*>(bsp::row_dist<double>),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(bsp::ND_LDS));
     if (e == hipSuccess) {
-        hipLaunchKernelGGL(bsp::medoid_dist, rows_grid, dim3(256), 0, nullptr, vecs, n, dim, dstride, d_cent, d_dist,
-                           d_best);
+        hipLaunchKernelGGL(bsp::row_dist<double>, rows_grid, dim3(256), bsp::ND_LDS, nullptr, vecs, n, dim, dstride,
+                           d_cent, d_dist, d_best);
         e = hipGetLastError();
     }
     if (e == hipSuccess) {
