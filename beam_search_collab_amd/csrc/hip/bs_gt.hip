@@ -6,7 +6,9 @@
 //   gt_norms    |b_j|^2 in fp32 and max_j |b_j|^2
 //   gt_select   32 queries x 32 rows per v_mfma_f32_32x32x2f32 step: a_j = |b_j|^2 - 2 q.b_j
 //               (fp32), the 128 smallest (a_j, j) per (query, row split) kept in HBM with a
-//               per-query threshold in registers and an LDS append buffer
+//               per-query threshold in registers and an LDS append buffer; each split
+//               publishes its 128th value per query (an upper bound of the query's 128th
+//               value over all rows) and filters by the least bound published
 //   gt_refine   merge the splits' lists, exact fp64 distances of the 128 candidates summed
 //               in dimension order (the host bs_groundtruth's arithmetic), order by
 //               (distance, id), and a certificate: every other row j has
@@ -37,8 +39,9 @@ using bsw::readlane64;
 using bsw::wave_sync;
 
 constexpr uint32_t C = 128;           // candidates kept per (query, split)
-constexpr uint32_t BUF = 64;          // LDS append slots per query
-constexpr uint32_t LDS_WAVE = 32 * BUF * 8 + 32 * 4 + 128 * 8 + 72 * 8;  // buffers, counts, merge
+constexpr uint32_t BUF = 128;         // LDS append slots per query
+constexpr uint32_t FLUSH = BUF - 32;  // a buffer is merged once it holds this many keys
+constexpr uint32_t LDS_WAVE = 32 * BUF * 8 + 128 * 8 + 72 * 8;  // append buffers, merge scratch
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
@@ -65,7 +68,7 @@ __device__ __forceinline__ uint32_t acc_row(int r, uint32_t half) {
 template <int KP>
 __global__ void __launch_bounds__(256) gt_select(const float* vecs, uint32_t dstride, const float* bn, uint64_t n,
                                                  const float* queries, uint32_t dim, uint64_t nq, uint32_t nsplit,
-                                                 uint64_t split_rows, uint64_t* topc) {
+                                                 uint64_t split_rows, uint64_t* topc, uint32_t* tshare) {
     constexpr int H = KP / 2;  // dimensions per lane half
     extern __shared__ __attribute__((aligned(16))) char smem[];
     const uint32_t lane = lane_id(), wave = threadIdx.x >> 6, half = lane >> 5, l32 = lane & 31u;
@@ -80,8 +83,7 @@ __global__ void __launch_bounds__(256) gt_select(const float* vecs, uint32_t dst
 
     char* my = smem + static_cast<size_t>(wave) * LDS_WAVE;
     uint64_t* buf = reinterpret_cast<uint64_t*>(my);
-    uint32_t* cnt = reinterpret_cast<uint32_t*>(my + 32 * BUF * 8);
-    uint64_t* mscr = reinterpret_cast<uint64_t*>(my + 32 * BUF * 8 + 32 * 4);
+    uint64_t* mscr = reinterpret_cast<uint64_t*>(my + 32 * BUF * 8);
     uint64_t* maux = mscr + 128;
 
     // A operand: lane (l32, half) holds query qb*32 + l32, dimensions half*H + t
@@ -105,8 +107,8 @@ __global__ void __launch_bounds__(256) gt_select(const float* vecs, uint32_t dst
     float tau[16];
 #pragma unroll
     for (int r = 0; r < 16; ++r) tau[r] = __builtin_inff();
-    if (lane < 32) cnt[lane] = 0;
-    wave_sync();
+    // lane i < 32 holds the number of keys in query i's append buffer
+    uint32_t cnt = 0;
     // queries whose list has been written to HBM (each lane re-reads only what it wrote)
     uint32_t written = 0;
 
@@ -126,7 +128,7 @@ __global__ void __launch_bounds__(256) gt_select(const float* vecs, uint32_t dst
 
     // merge every query buffer holding at least `need` keys into its top-C list
     auto compact = [&](uint32_t need) __attribute__((always_inline)) {
-        const uint32_t mycnt = lane < 32 ? cnt[lane] : 0u;
+        const uint32_t mycnt = lane < 32 ? cnt : 0u;
         uint64_t todo = ballot(lane < 32 && mycnt >= need);
         while (todo) {
             const uint32_t i = static_cast<uint32_t>(__builtin_ctzll(todo));
@@ -136,24 +138,32 @@ __global__ void __launch_bounds__(256) gt_select(const float* vecs, uint32_t dst
             if (qi < nq) {
                 uint64_t* top = topc + (qi * nsplit + s) * C;
                 uint64_t beam[2] = {EMPTY_KEY, EMPTY_KEY};
+                const uint32_t shared = tshare[qi];  // issued with the list: one round trip
                 if ((written >> i) & 1u) {
                     beam[0] = top[lane];
                     beam[1] = top[64 + lane];
                 }
                 written |= 1u << i;
-                uint64_t ck[1] = {lane < c ? buf[i * BUF + lane] : EMPTY_KEY};
-                uint64_t cm[1] = {ballot(lane < c)};
-                bsd::beam_merge<2, 1, true>(beam, ck, cm, C, mscr, maux);
+                // one HBM round trip of the list per flush, then the buffer in runs of 64
+                for (uint32_t b0 = 0; b0 < c; b0 += 64) {
+                    uint64_t ck[1] = {b0 + lane < c ? buf[i * BUF + b0 + lane] : EMPTY_KEY};
+                    uint64_t cm[1] = {ballot(b0 + lane < c)};
+                    bsd::beam_merge<2, 1, true>(beam, ck, cm, C, mscr, maux);
+                }
                 top[lane] = beam[0];
                 top[64 + lane] = beam[1];
                 const uint64_t last = readlane64(beam[1], 63);
-                const float nt = last == EMPTY_KEY ? __builtin_inff() : bsd::key_dist(last);
+                // this split's C-th value bounds the query's C-th value over all rows from
+                // above; publish it, and filter by the least bound any split has published
+                if (last != EMPTY_KEY && lane == 0) atomicMin(&tshare[qi], static_cast<uint32_t>(last >> 32));
+                const uint32_t tk = std::min(last == EMPTY_KEY ? ~0u : static_cast<uint32_t>(last >> 32), shared);
+                const float nt = tk == ~0u ? __builtin_inff() : bsd::key_dist(static_cast<uint64_t>(tk) << 32);
                 const uint32_t rr = 4u * (i / 8u) + (i % 4u), hh = (i / 4u) & 1u;
 #pragma unroll
                 for (int r = 0; r < 16; ++r)
                     if (static_cast<uint32_t>(r) == rr && half == hh) tau[r] = nt;
             }
-            if (lane == 0) cnt[i] = 0;
+            if (lane == i) cnt = 0;
             wave_sync();
         }
     };
@@ -171,17 +181,48 @@ __global__ void __launch_bounds__(256) gt_select(const float* vecs, uint32_t dst
         }
         const uint64_t j = tile + l32;
         const bool whole = tile + 32 <= r1;  // wave-uniform: only a split's last tile is partial
+        // Accumulator register r holds, in each lane half h, the 32 rows of one query
+        // acc_row(r, h), so a register's survivors append to at most two buffers: their
+        // slots come from the ballot (mbcnt within the half), not from LDS atomics.  First
+        // every a_j and the survivors (independent, so they issue back to back), then the
+        // wave-uniform branches, only for groups of four registers holding a survivor.
+        float av[16];
+        uint32_t okb = 0;
+        const bool in = whole || j < r1;
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-            const float av = __builtin_fmaf(-2.0f, acc[r], bnj);
-            if (av <= tau[r] && (whole || j < r1)) {
-                const uint32_t i = acc_row(r, half);
-                const uint32_t pos = atomicAdd(&cnt[i], 1u);  // < BUF: see compact(32) below
-                buf[i * BUF + pos] = (static_cast<uint64_t>(orderable(av)) << 32) | static_cast<uint32_t>(j);
+            av[r] = __builtin_fmaf(-2.0f, acc[r], bnj);
+            okb |= (in && av[r] <= tau[r]) ? 1u << r : 0u;
+        }
+        const uint64_t any = ballot(okb != 0u);
+        bool appended = false;
+        if (any) {
+            appended = true;
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                if (!ballot(((okb >> (4 * g)) & 15u) != 0u)) continue;
+#pragma unroll
+                for (int r = 4 * g; r < 4 * g + 4; ++r) {
+                    const bool ok = (okb >> r) & 1u;
+                    const uint64_t m = ballot(ok);
+                    if (!m) continue;
+                    const uint32_t m0 = static_cast<uint32_t>(m), m1 = static_cast<uint32_t>(m >> 32);
+                    const uint32_t i0 = acc_row(r, 0), i1 = acc_row(r, 1);
+                    const uint32_t c0 = readlane(cnt, i0), c1 = readlane(cnt, i1);  // < FLUSH: see below
+                    if (ok) {
+                        const uint32_t pos = half ? c1 + __builtin_amdgcn_mbcnt_hi(m1, 0u) : c0 + __builtin_amdgcn_mbcnt_lo(m0, 0u);
+                        const uint32_t i = half ? i1 : i0;
+                        buf[i * BUF + pos] = (static_cast<uint64_t>(orderable(av[r])) << 32) | static_cast<uint32_t>(j);
+                    }
+                    cnt += lane == i0 ? static_cast<uint32_t>(__builtin_popcount(m0)) : 0u;
+                    cnt += lane == i1 ? static_cast<uint32_t>(__builtin_popcount(m1)) : 0u;
+                }
             }
         }
-        wave_sync();
-        compact(32);  // every buffer holds < 32 keys before the next 32 rows arrive
+        if (appended) {
+            wave_sync();
+            compact(FLUSH);  // every buffer holds < FLUSH keys before the next 32 rows arrive
+        }
     };
 
     float4 bA[H / 4], bB[H / 4];
@@ -308,12 +349,12 @@ int gfail(int code, const std::string& msg) {
 template <int KP>
 hipError_t launch_select(dim3 g, hipStream_t s, const float* vecs, uint32_t dstride, const float* bn, uint64_t n,
                          const float* q, uint32_t dim, uint64_t nq, uint32_t nsplit, uint64_t split_rows,
-                         uint64_t* topc) {
+                         uint64_t* topc, uint32_t* tshare) {
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(bsg::gt_select<KP>),
                                        hipFuncAttributeMaxDynamicSharedMemorySize, 4 * bsg::LDS_WAVE);
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL(bsg::gt_select<KP>, g, dim3(256), 4 * bsg::LDS_WAVE, s, vecs, dstride, bn, n, q, dim, nq,
-                       nsplit, split_rows, topc);
+                       nsplit, split_rows, topc, tshare);
     return hipGetLastError();
 }
 }  // namespace
@@ -344,20 +385,24 @@ extern "C" int bs_index_groundtruth_device(bs_index idx, const float* d_queries,
     float* bn = nullptr;
     uint32_t* bmax = nullptr;
     uint64_t* topc = nullptr;
+    uint32_t* tshare = nullptr;
     unsigned long long* nunc = nullptr;
     auto release = [&]() {
         if (bn) (void)hipFree(bn);
         if (bmax) (void)hipFree(bmax);
         if (topc) (void)hipFree(topc);
+        if (tshare) (void)hipFree(tshare);
         if (nunc) (void)hipFree(nunc);
     };
     if (hipMalloc(&bn, n * sizeof(float)) != hipSuccess || hipMalloc(&bmax, 4) != hipSuccess ||
-        hipMalloc(&topc, nq * nsplit * bsg::C * 8) != hipSuccess || hipMalloc(&nunc, 8) != hipSuccess) {
+        hipMalloc(&topc, nq * nsplit * bsg::C * 8) != hipSuccess || hipMalloc(&nunc, 8) != hipSuccess ||
+        hipMalloc(&tshare, nq * 4) != hipSuccess) {
         release();
         return gfail(BS_ENOMEM, "hipMalloc of the ground-truth work buffers failed");
     }
     hipError_t e = hipMemsetAsync(bmax, 0, 4, s);
     if (e == hipSuccess) e = hipMemsetAsync(nunc, 0, 8, s);
+    if (e == hipSuccess) e = hipMemsetAsync(tshare, 0xFF, nq * 4, s);  // no bound published yet
     if (e == hipSuccess) {
         hipLaunchKernelGGL(bsg::gt_norms, dim3(static_cast<uint32_t>((n + 255) / 256)), dim3(256), 0, s, vecs, n, dim,
                            dstride, bn, bmax);
@@ -371,10 +416,10 @@ extern "C" int bs_index_groundtruth_device(bs_index idx, const float* d_queries,
     if (e == hipSuccess) {
         const dim3 g(static_cast<uint32_t>((nqb * nsplit + 3) / 4));
         switch (KP) {
-        case 64: e = launch_select<64>(g, s, vecs, dstride, bn, n, d_queries, dim, nq, nsplit, split_rows, topc); break;
-        case 128: e = launch_select<128>(g, s, vecs, dstride, bn, n, d_queries, dim, nq, nsplit, split_rows, topc); break;
-        case 192: e = launch_select<192>(g, s, vecs, dstride, bn, n, d_queries, dim, nq, nsplit, split_rows, topc); break;
-        default: e = launch_select<256>(g, s, vecs, dstride, bn, n, d_queries, dim, nq, nsplit, split_rows, topc); break;
+        case 64: e = launch_select<64>(g, s, vecs, dstride, bn, n, d_queries, dim, nq, nsplit, split_rows, topc, tshare); break;
+        case 128: e = launch_select<128>(g, s, vecs, dstride, bn, n, d_queries, dim, nq, nsplit, split_rows, topc, tshare); break;
+        case 192: e = launch_select<192>(g, s, vecs, dstride, bn, n, d_queries, dim, nq, nsplit, split_rows, topc, tshare); break;
+        default: e = launch_select<256>(g, s, vecs, dstride, bn, n, d_queries, dim, nq, nsplit, split_rows, topc, tshare); break;
         }
     }
     if (e == hipSuccess) {
