@@ -183,6 +183,12 @@ __global__ void __launch_bounds__(256) vb_search(const Graph G, const uint32_t* 
             if (fresh) d = l2_seq(G.vecs + static_cast<uint64_t>(nb) * G.dstride, trow, G.dim);
             const uint64_t ck = fresh ? bsd::make_key(d, nb) : EMPTY_KEY;
             uint64_t m = ballot(fresh);
+            if (sz == L && m) {
+                // a full beam's last entry only moves closer, so a candidate at or beyond it
+                // now is refused at its turn as well: only the others go through the pushes
+                const float dl = bsd::key_dist(beam_at<TR>(beam, L - 1));
+                m &= ballot(fresh && d < dl);
+            }
             while (m) {
                 const uint32_t l = static_cast<uint32_t>(__builtin_ctzll(m));
                 m &= m - 1;
@@ -244,9 +250,46 @@ __device__ void prune_list(const Graph& G, uint64_t* keys, uint32_t n, uint32_t 
     }
     uint32_t kc = 0;
     const float alphas[2] = {1.0f, alpha};
+    const uint32_t h = lane >> 5, l = lane & 31u;
     for (int pass = 0; pass < 2; ++pass) {
         const float a = alphas[pass];
-        for (uint32_t i = 0; i < nu && kc < G.deg; ++i) {
+        uint32_t i = 0;
+        while (i < nu && kc < G.deg) {
+            if (kc <= 32) {
+                // Two candidates per step: lanes 0-31 test e_i and lanes 32-63 test e_(i+1)
+                // against the kept set (one kept node per lane), so all lanes are busy.  When
+                // e_i is kept, e_(i+1) is also tested against e_i before it can be kept, so
+                // every decision is the one-at-a-time loop's, on the same distances.
+                const bool two = i + 1 < nu;
+                const uint64_t e = keys[two ? i + h : i];
+                bool hit = false;
+                if (l < kc && (h == 0 || two)) {
+                    const float* erow = G.vecs + static_cast<uint64_t>(static_cast<uint32_t>(e)) * G.dstride;
+                    const uint32_t kid = static_cast<uint32_t>(kept[l]);
+                    hit = a * l2_seq(erow, G.vecs + static_cast<uint64_t>(kid) * G.dstride, G.dim) <= lkey_dist(e);
+                }
+                const uint64_t bm = ballot(hit);
+                const uint64_t e0 = readlane64(e, 0), e1 = readlane64(e, 32);
+                bool dom1 = (bm >> 32) != 0ull;
+                if ((bm & 0xFFFFFFFFull) == 0ull) {
+                    if (lane == 0) kept[kc] = e0;
+                    ++kc;
+                    wave_sync();
+                    if (two && kc < G.deg && !dom1) {
+                        const float d = l2_seq(G.vecs + static_cast<uint64_t>(static_cast<uint32_t>(e1)) * G.dstride,
+                                               G.vecs + static_cast<uint64_t>(static_cast<uint32_t>(e0)) * G.dstride, G.dim);
+                        dom1 = a * d <= lkey_dist(e1);
+                    }
+                }
+                if (two && kc < G.deg && !dom1) {
+                    if (lane == 0) kept[kc] = e1;
+                    ++kc;
+                    wave_sync();
+                }
+                i += two ? 2 : 1;
+                continue;
+            }
+            // more than 32 kept: one candidate, a kept node per lane in chunks of 64
             const uint64_t e = keys[i];
             const uint32_t eid = static_cast<uint32_t>(e);
             const float ed = lkey_dist(e);
@@ -266,6 +309,7 @@ __device__ void prune_list(const Graph& G, uint64_t* keys, uint32_t n, uint32_t 
                 ++kc;
                 wave_sync();
             }
+            ++i;
         }
     }
     for (uint32_t i = lane; i < kc; i += 64) {
