@@ -51,8 +51,11 @@ __device__ __forceinline__ uint32_t orderable(float f) {
 // restructure.  The compiler does not count them, so every result is claimed through
 // lgkm_wait (at most N LDS operations of this wavefront still outstanding, the register
 // tied to the wait so no use moves above it) or lgkm_drain before it is read or its
-// registers are reused.  Only the wavefront's own LDS operations count: LDS returns in
-// issue order, so waiting down to N completes all but the N most recent.
+// registers are reused.  LDS returns in issue order, so waiting down to N completes all
+// but the N most recent of these reads (scalar loads the compiler has in flight only make
+// the wait longer).  The compiler must not copy such a register before its wait: the
+// generated code reads each one in place, and the entry-point tests compare the centroid's
+// node bit for bit with the host restatement.
 __device__ __forceinline__ uint32_t lds_address(const float* p) {
     return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((const __attribute__((address_space(3))) float*)p));
 }
