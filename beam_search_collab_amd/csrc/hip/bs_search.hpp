@@ -300,10 +300,24 @@ search_kernel(const SearchParams p) {
             }
             constexpr int NC = WIDE ? 4 : CR;
             uint4 cw[NC];
+            // Narrow codes (4 words per neighbour, one candidate register): two lanes per
+            // neighbour, two words each -- lane l takes words 2 (l / 32), 2 (l / 32) + 1 of
+            // neighbour l % 32 (and of neighbour 32 + l % 32 when R > 32) -- so the popcounts
+            // of a 32-neighbour row run on every lane; lanes l and l + 32 add their halves.
+            constexpr bool HALVES = !WIDE && CR == 1;
+            uint2 ca = make_uint2(0u, 0u), cb = make_uint2(0u, 0u);
+            if constexpr (HALVES) {
+                const uint32_t nb = lane & 31u, w = 2u * (lane >> 5);
+                ca = *reinterpret_cast<const uint2*>(codes + static_cast<uint64_t>(nb < p.R ? nb : 0u) * S.cws + w);
+                if (p.R > 32u)
+                    cb = *reinterpret_cast<const uint2*>(
+                        codes + static_cast<uint64_t>(nb + 32u < p.R ? nb + 32u : 0u) * S.cws + w);
+            } else {
 #pragma unroll
-            for (int t = 0; t < NC; ++t) {
-                const uint32_t nb = WIDE ? static_cast<uint32_t>(t) * S.npp + nl : static_cast<uint32_t>(t) * 64u + lane;
-                cw[t] = load_quad(codes, nb, p.R, qi, S);
+                for (int t = 0; t < NC; ++t) {
+                    const uint32_t nb = WIDE ? static_cast<uint32_t>(t) * S.npp + nl : static_cast<uint32_t>(t) * 64u + lane;
+                    cw[t] = load_quad(codes, nb, p.R, qi, S);
+                }
             }
 
             // exact distance of the parent
@@ -320,6 +334,26 @@ search_kernel(const SearchParams p) {
                 for (int rc = 0; rc < CR; ++rc) {
                     const uint32_t i = static_cast<uint32_t>(rc) * 64u + lane;
                     raw[rc] = rawbuf[i < p.R ? i : 0u];
+                }
+            } else if constexpr (HALVES) {
+                const uint32_t* pw = planes4 + 2u * (lane >> 5);
+                uint2 w[6];
+#pragma unroll
+                for (int b = 0; b < 6; ++b) w[b] = *reinterpret_cast<const uint2*>(pw + 4 * b);
+                auto half_sum = [&](uint2 c) __attribute__((always_inline)) {
+                    uint32_t r = 0;
+#pragma unroll
+                    for (int b = 0; b < 6; ++b) {
+                        uint32_t n = static_cast<uint32_t>(__builtin_popcount(w[b].x & c.x));
+                        n += static_cast<uint32_t>(__builtin_popcount(w[b].y & c.y));
+                        r += n << b;
+                    }
+                    return r + bsw::xor_lane<32>(r);
+                };
+                raw[0] = half_sum(ca);
+                if (p.R > 32u) {
+                    const uint32_t rb = half_sum(cb);
+                    raw[0] = lane < 32u ? raw[0] : rb;
                 }
             } else {
 #pragma unroll
