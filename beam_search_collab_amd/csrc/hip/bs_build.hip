@@ -206,12 +206,6 @@ __global__ void __launch_bounds__(256) vb_search(const Graph G, const uint32_t* 
 // dedupe_and_prune (build_graph.cpp:156-208) of one sorted list of list keys, a
 // wavefront per list; the result becomes node src's list.  keys are rewritten in place
 // (the deduplicated prefix).  kept: LDS, deg entries per wavefront.
-struct PruneJob {
-    const uint64_t* keys;  // sorted (dist, node)
-    uint32_t n;
-    uint32_t src;
-};
-
 __device__ void prune_list(const Graph& G, uint64_t* keys, uint32_t n, uint32_t src, float alpha, uint64_t* kept) {
     const uint32_t lane = lane_id();
     // dedupe: skip src and an id equal to the last kept one (in place, order kept)
