@@ -411,16 +411,13 @@ int make_plan(bs_index ix, const bs_search_cfg* cfg, uint64_t nq, Plan& pl) {
     p.max_it = cfg->max_iterations;
     p.reset = cfg->reset_interval;
     p.L = L;
-    uint32_t filter_bytes;
-    if (mode == BS_GROUP_BLOOM) {
-        uint32_t b = log2_ceil(cap);
-        if (b < 5) b = 5;
-        p.filter_bits = b;
-        filter_bytes = (1u << (b - 5)) * 4;
-    } else {
-        p.filter_bits = log2_ceil(cap);
-        filter_bytes = (1u << p.filter_bits) * 4;
-    }
+    // The hash filters (visit filter, RaBitQ expanded set) refuse keys as the reference's
+    // table of 2^ceil(log2 capacity) slots does, but get twice as many slots (up to 2048)
+    // when the workgroup's LDS allows it: probe runs at the same occupancy are shorter, the
+    // results are the same.  The visit filter fills up between resets (config B: 5.0 -> 4.8
+    // ms, topk 512: 20.1 -> 10.9 ms); the RaBitQ expanded set holds about 1.2 T keys, so it
+    // is doubled only past T = 0.4 x slots (topk 768: 22.4 -> 14.7 ms), since at topk 256
+    // the larger table costs more wavefronts per CU than it saves (3.35 -> 3.5 ms).
     uint32_t scratch = 512u * pl.TR;
     if (mode == BS_RABITQ) {
         p.pdim = ix->pdim;
@@ -436,13 +433,33 @@ int make_plan(bs_index ix, const bs_search_cfg* cfg, uint64_t nq, Plan& pl) {
         scratch = planes_at + 24u * std::max(ix->wpp, 4u);
         p.off_planes = planes_at;  // relative to off_scratch until the layout is fixed below
     }
+    const uint32_t planes_rel = p.off_planes;
     auto al = [](uint32_t v) { return (v + 15u) & ~15u; };
-    p.off_filter = 0;
-    p.off_scratch = al(filter_bytes);
-    p.off_cand = p.off_scratch + al(scratch);
-    if (mode == BS_RABITQ) p.off_planes += p.off_scratch;
-    p.off_coop = p.off_cand + 64u * pl.CR * 8u + 8u * std::max(pl.TR, 8);  // after the merge's slot bitmap
-    p.lds_wave = al(p.off_coop + 4u);
+    auto layout = [&](uint32_t filter_bytes) {
+        p.off_filter = 0;
+        p.off_scratch = al(filter_bytes);
+        p.off_cand = p.off_scratch + al(scratch);
+        if (mode == BS_RABITQ) p.off_planes = planes_rel + p.off_scratch;
+        p.off_coop = p.off_cand + 64u * pl.CR * 8u + 8u * std::max(pl.TR, 8);  // after the merge's slot bitmap
+        p.lds_wave = al(p.off_coop + 4u);
+    };
+    if (mode == BS_GROUP_BLOOM) {
+        uint32_t b = log2_ceil(cap);
+        if (b < 5) b = 5;
+        p.filter_bits = b;
+        p.filter_cap = 0;
+        layout((1u << (b - 5)) * 4);
+    } else {
+        const uint32_t b = log2_ceil(cap);
+        p.filter_cap = 1u << b;
+        const bool grow = b < 11 && (mode != BS_RABITQ || 5ull * T > 2ull * p.filter_cap);
+        p.filter_bits = grow ? b + 1 : b;
+        layout((1u << p.filter_bits) * 4);
+        if (static_cast<size_t>(p.lds_wave) * ny > ix->max_lds && p.filter_bits > b) {
+            p.filter_bits = b;
+            layout((1u << b) * 4);
+        }
+    }
     // base mode with too few queries to give every SIMD 4 wavefronts: 2 or 4 wavefronts
     // share one query (the reference's block-per-query base kernel); they split the
     // distance rows of each expansion, the rest of the loop runs on the first wavefront.

@@ -326,6 +326,7 @@ __global__ void __launch_bounds__(64) dbg_filter_kernel(int bloom, uint32_t bits
         h.bits = bits;
         h.size = 1u << bits;
         h.mask = h.size - 1;
+        h.cap = h.size;
         h.clear();
         for (uint32_t b = 0; b < nbatch; ++b) {
             const uint32_t k = lane < bsize ? keys[static_cast<uint64_t>(b) * bsize + lane] : bsd::INVALID;

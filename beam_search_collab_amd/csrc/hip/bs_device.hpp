@@ -325,9 +325,14 @@ __device__ __forceinline__ void sort_beam(uint64_t (&v)[TR]) {
 
 // HashFilter (filter_hash.cuh:11-99): 2^bits slots, h = (k ^ (k >> bits)) & mask, linear
 // probing, empty = 0xFFFFFFFF.  `occ` counts occupied slots (wave-uniform).
+// The reference's table (filter_hash.cuh) has cap = 2^ceil(log2 capacity) slots and refuses
+// keys once full; membership itself does not depend on where keys sit, so this table may
+// have more slots (size >= cap) for shorter probe runs and still refuse exactly the keys
+// the reference refuses: the occupancy is checked against cap.
 struct HashLds {
     uint32_t* t;
     uint32_t bits, size, mask;
+    uint32_t cap;
     uint32_t occ;
 
     __device__ __forceinline__ uint32_t slot0(uint32_t k) const { return (k ^ (k >> bits)) & mask; }
@@ -343,7 +348,7 @@ struct HashLds {
     // step, first slot that holds k (present) or is empty (insert there).
     // returns 1 if newly inserted; 0 if present or the table is full.
     __device__ __forceinline__ uint32_t insert1(uint32_t k) {
-        if (occ >= size) return 0u;  // full: present or rejected, 0 either way
+        if (occ >= cap) return 0u;  // full: present or rejected, 0 either way
         const uint32_t lane = lane_id();
         const uint32_t h = slot0(k);
         for (uint32_t base = 0; base < size; base += 64) {
@@ -388,8 +393,8 @@ struct HashLds {
         uint32_t isnew = 0;
         // A full table accepts nothing and every key already present reports 0, so the
         // batch changes nothing (filter_hash.cuh:78-86 probes all slots to the same end).
-        if (nv == 0 || occ >= size) return 0;
-        if (occ + nv <= size) {
+        if (nv == 0 || occ >= cap) return 0;
+        if (occ + nv <= cap) {
             uint32_t idx = slot0(k);
             bool done = !valid;
             for (uint32_t step = 0; step <= size; ++step) {
@@ -411,7 +416,7 @@ struct HashLds {
         } else {
             // lane order until the table fills; the keys after that all report 0
             uint64_t m = vm;
-            while (m && occ < size) {
+            while (m && occ < cap) {
                 const uint32_t l = static_cast<uint32_t>(__builtin_ctzll(m));
                 m &= m - 1;
                 const uint32_t r = insert1(readlane(k, l));

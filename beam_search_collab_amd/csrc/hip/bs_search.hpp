@@ -27,6 +27,7 @@ struct SearchParams {
     uint64_t nq;
     uint32_t dim, dstride, R, K, T;
     uint32_t filter_bits;   // hash: log2 slots; bloom: log2 bits
+    uint32_t filter_cap;    // hash: keys the table accepts (the reference's slot count)
     uint32_t entry;
     int32_t max_it, reset;
     uint32_t pdim, wpp, rec_words, rec_ids, rec_fac, rec_codes;  // record offsets (words)
@@ -102,6 +103,7 @@ search_kernel(const SearchParams p) {
             hf.bits = p.filter_bits;
             hf.size = 1u << p.filter_bits;
             hf.mask = hf.size - 1;
+            hf.cap = p.filter_cap;
             hf.clear();
         } else {
             bf.w = reinterpret_cast<uint32_t*>(my + p.off_filter);
@@ -237,6 +239,7 @@ search_kernel(const SearchParams p) {
         hf.bits = p.filter_bits;
         hf.size = 1u << p.filter_bits;
         hf.mask = hf.size - 1;
+        hf.cap = p.filter_cap;
         const uint32_t wpp = p.wpp;
         const uint64_t rstride = p.rec_words;
         const float* rbase = reinterpret_cast<const float*>(p.recs);
@@ -401,10 +404,10 @@ search_kernel(const SearchParams p) {
 
         // dedup flush from the smallest (gpu_search_rabitq.cuh:319-339): identical ids
         // carry identical exact distances and are adjacent; the flush's hash set accepts
-        // at most `size` distinct ids.
+        // at most `cap` distinct ids (the reference's slot count).
         uint32_t* out = p.results + qid * p.K;
         float* dout = p.dists ? p.dists + qid * p.K : nullptr;
-        const uint32_t limit = (p.K < hf.size) ? p.K : hf.size;
+        const uint32_t limit = (p.K < hf.cap) ? p.K : hf.cap;
         uint32_t written = 0;
         uint32_t prev_last = INVALID;  // id of element 64*r - 1
         uint32_t wpos[TR];
