@@ -484,10 +484,12 @@ struct BloomLds {
             present[rc] = (k[rc] != INVALID) ? test_lane(k[rc]) : true;
             dup[rc] = false;
         }
-        // first occurrence: compare against every earlier valid key
+        // first occurrence among the keys not yet present: a key equal to one of them hashes
+        // to the same bits and was tested on the same table, so it is absent too, and only
+        // absent keys can be new
 #pragma unroll
         for (int rj = 0; rj < CR; ++rj) {
-            uint64_t m = ballot(k[rj] != INVALID);
+            uint64_t m = ballot(k[rj] != INVALID && !present[rj]);
             while (m) {
                 const uint32_t lj = static_cast<uint32_t>(__builtin_ctzll(m));
                 m &= m - 1;
