@@ -10,7 +10,7 @@ is one search of all queries with the queries already resident in HBM.
                     [--topk 256] [--K 100] [--sweep 64,128,512] [--sweep-modes warp2,bwarp2]
                     [--no-cpu]
 
---config selects the other synthetic workloads of the survey (A: 100k x 128 topk 64;
+--config selects the other synthetic workloads of the benchmark configs (A: 100k x 128 topk 64;
 C: B + rabitq codebook seed 12345, K=10; D: 1.2M x 100 N(0,1) L2-normalised, degree 64,
 topk 128, K=10, warp1; E: 1M x 960, 256 centres ~U[0,1], sigma 0.05, 1k queries).
 

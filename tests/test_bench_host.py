@@ -30,7 +30,7 @@ def test_kernel_name_matches_instance_rules():
     assert bench.kernel_name("base", 768, 32, 128) == "bsd::search_kernel<16, 1, 4, 0, 2>"
 
 
-def test_configs_follow_the_survey():
+def test_configs_match_the_benchmark_configs():
     c = bench.CONFIGS
     assert (c["B"]["n"], c["B"]["dim"], c["B"]["degree"], c["B"]["topk"], c["B"]["K"]) == (1_000_000, 128, 32, 256, 100)
     assert c["C"]["mode"] == "rabitq" and c["C"]["K"] == 10
