@@ -115,17 +115,30 @@ __global__ void __launch_bounds__(64) dbg_fastscan_kernel(const float* query, co
     const uint32_t lane = bsd::lane_id();
     const uint32_t wpp = pdim / 32u;
     const bsd::QuantOut qo = bsd::quantize(query, signs, dim, pdim, seed, scr, planes, codes_out);
-    // codes_nbr: nn neighbours of cws = max(wpp, 4) words each (the record layout)
+    // codes_nbr: nn neighbours of cws = max(wpp, 4) words each (the record layout).  The
+    // search kernel's paths: narrow codes with nn <= 64 (one candidate register) two lanes
+    // per neighbour; narrow codes with nn > 64 a neighbour per lane and register; wide codes
+    // pdim / 128 lanes per neighbour.
     const bsd::QuadShape S = bsd::quad_shape(wpp, nn);
     uint4 pl[6];
     if (S.qpn == 1) {
         // narrow: the shared plane words go through LDS as in the search kernel
-        uint32_t* planes4 = reinterpret_cast<uint32_t*>(smem + ((4u * pdim + 24u * wpp + 256u + 15u) & ~15u));
+        uint32_t* planes4 = reinterpret_cast<uint32_t*>(smem + ((4u * pdim + 24u * wpp + 512u + 15u) & ~15u));
         bsd::store_planes4(planes, wpp, planes4);
+        if (nn <= 64u) {
+            const bsd::CodeHalves h = bsd::load_code_halves(codes_nbr, nn, S);
+            const uint32_t r = bsd::raw_halves(planes4, h, nn);
+            if (lane < nn) rawbuf[lane] = r;
+        } else {
 #pragma unroll
-        for (int b = 0; b < 6; ++b) pl[b] = reinterpret_cast<const uint4*>(planes4)[b];
-        const uint32_t r = bsd::raw_quad(pl, bsd::load_quad(codes_nbr, lane, nn, 0u, S));
-        if (lane < nn) rawbuf[lane] = r;
+            for (int b = 0; b < 6; ++b) pl[b] = reinterpret_cast<const uint4*>(planes4)[b];
+#pragma unroll
+            for (uint32_t rc = 0; rc < 2; ++rc) {
+                const uint32_t nb = rc * 64u + lane;
+                const uint32_t r = bsd::raw_quad(pl, bsd::load_quad(codes_nbr, nb, nn, 0u, S));
+                if (nb < nn) rawbuf[nb] = r;
+            }
+        }
         bsd::wave_sync();
     } else {
         bsd::lane_plane_quads(planes, wpp, S, pl);
@@ -135,11 +148,11 @@ __global__ void __launch_bounds__(64) dbg_fastscan_kernel(const float* query, co
         for (int t = 0; t < 4; ++t) c0[t] = bsd::load_quad(codes_nbr, static_cast<uint32_t>(t) * S.npp + nl, nn, qi, S);
         bsd::raw_sums_wide(pl, codes_nbr, nn, S, c0, rawbuf);
     }
-    if (lane < nn) {
-        const uint32_t raw = rawbuf[lane];
-        raw_out[lane] = raw;
-        est_out[lane] = bsd::estimate(raw, qo.sum_q, qo.width, qo.low, factors[lane], factors[degree + lane],
-                                      factors[2 * degree + lane], exact);
+    for (uint32_t j = lane; j < nn; j += 64) {
+        const uint32_t raw = rawbuf[j];
+        raw_out[j] = raw;
+        est_out[j] = bsd::estimate(raw, qo.sum_q, qo.width, qo.low, factors[j], factors[degree + j],
+                                   factors[2 * degree + j], exact);
     }
     if (lane == 0) {
         scal_out[0] = qo.low;
@@ -155,7 +168,7 @@ extern "C" int bs_debug_fastscan(const float* query, const float* signs, uint32_
     uint32_t pdim = 1;
     while (pdim < dim) pdim <<= 1;
     if (pdim < 32 || pdim > 2048) return dfail(BS_EINVAL, "padded dim must be in 32..2048");
-    if (nn == 0 || nn > 64 || nn > degree) return dfail(BS_EINVAL, "need 1 <= nn <= min(64, degree)");
+    if (nn == 0 || nn > 128 || nn > degree) return dfail(BS_EINVAL, "need 1 <= nn <= min(128, degree)");
     const uint32_t wpp = pdim / 32;
     DevBuf<float> dq, ds, dfac, dscal, dest;
     DevBuf<uint32_t> dcodes, draw;
@@ -178,7 +191,7 @@ extern "C" int bs_debug_fastscan(const float* query, const float* signs, uint32_
     DTRY(hipMemcpy(ds.p, signs, pdim * 4, hipMemcpyHostToDevice));
     DTRY(hipMemcpy(dfac.p, factors, 3 * degree * 4, hipMemcpyHostToDevice));
     DTRY(hipMemcpy(dcodes.p, padded.data(), padded.size() * 4, hipMemcpyHostToDevice));
-    const size_t lds = ((4u * pdim + 24u * wpp + 4u * 64u + 15u) & ~15u) + 96u;
+    const size_t lds = ((4u * pdim + 24u * wpp + 4u * 128u + 15u) & ~15u) + 96u;
     hipLaunchKernelGGL(dbg_fastscan_kernel, dim3(1), dim3(64), lds, nullptr, dq.p, ds.p, dim, pdim, seed, dcodes.p,
                        dfac.p, nn, degree, exact, dco.p, dscal.p, dsum.p, draw.p, dest.p);
     DTRY(hipGetLastError());

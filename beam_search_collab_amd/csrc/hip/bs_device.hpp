@@ -382,9 +382,11 @@ struct HashLds {
     }
 
     // lane-parallel batch (one key per lane, INVALID = idle).  Sequential semantics in
-    // lane order: when the batch cannot fill the table, every lane inserts concurrently
-    // with LDS compare-and-swap (membership does not depend on the order); otherwise the
-    // keys are inserted one by one in lane order.  Returns 1 for newly inserted keys.
+    // lane order (DESC: from lane 63 down): when the batch cannot fill the table, every
+    // lane inserts concurrently with LDS compare-and-swap (membership does not depend on
+    // the order); otherwise the keys are inserted one by one in that order.  Returns 1 for
+    // newly inserted keys.
+    template <bool DESC = false>
     __device__ __forceinline__ uint32_t insert_batch(uint32_t k) {
         const uint32_t lane = lane_id();
         const bool valid = k != INVALID;
@@ -414,11 +416,12 @@ struct HashLds {
             wave_sync();
             occ += static_cast<uint32_t>(__builtin_popcountll(ballot(isnew != 0)));
         } else {
-            // lane order until the table fills; the keys after that all report 0
+            // one key at a time until the table fills; the keys after that all report 0
             uint64_t m = vm;
             while (m && occ < cap) {
-                const uint32_t l = static_cast<uint32_t>(__builtin_ctzll(m));
-                m &= m - 1;
+                const uint32_t l = DESC ? 63u - static_cast<uint32_t>(__builtin_clzll(m))
+                                        : static_cast<uint32_t>(__builtin_ctzll(m));
+                m &= ~(1ull << l);
                 const uint32_t r = insert1(readlane(k, l));
                 if (lane == l) isnew = r;
             }
@@ -427,10 +430,13 @@ struct HashLds {
     }
 };
 
-// BloomFilter (filter_bloom.cuh:13-131): 2^max(5, bits) bits, three hashes.  Batch
-// semantics (the reference's test-then-atomicOr races for a key inserted twice in one
-// step): a key is new iff its bits were not all set before the batch and it is the first
-// lane holding that value; then every key's bits are set.
+// BloomFilter (filter_bloom.cuh:13-131): 2^max(5, bits) bits, three hashes.  The
+// reference's warp filters a row in rounds of 32 neighbours (gpu_search_warp.cuh:203-205,
+// lane stride BX = 32), each lane testing its key's bits and then setting them
+// (filter_bloom.cuh:104-120), so a round's keys see the bits of every earlier round.
+// Within a round the test-then-atomicOr races for a key held twice; the rule here: a key
+// is new iff its bits were not all set before its round and it is the first index of the
+// round holding that value.
 struct BloomLds {
     uint32_t* w;
     uint32_t bits, words, mask;
@@ -474,41 +480,35 @@ struct BloomLds {
         atomicOr(&w[h2 >> 5], 1u << (h2 & 31));
     }
 
-    // keys k[rc] (rc-th register, index rc*64 + lane); returns new flags per register
+    // keys k[rc] (rc-th register, index rc*64 + lane); returns new flags per register.
+    // Rounds of 32 indices in index order: register rc's lanes 0-31, then its lanes 32-63.
     template <int CR>
     __device__ __forceinline__ void insert_batch(const uint32_t (&k)[CR], uint32_t (&isnew)[CR]) {
         const uint32_t lane = lane_id();
-        bool present[CR], dup[CR];
+        const bool upper = lane >= 32u;
 #pragma unroll
         for (int rc = 0; rc < CR; ++rc) {
-            present[rc] = (k[rc] != INVALID) ? test_lane(k[rc]) : true;
-            dup[rc] = false;
-        }
-        // first occurrence among the keys not yet present: a key equal to one of them hashes
-        // to the same bits and was tested on the same table, so it is absent too, and only
-        // absent keys can be new
+            isnew[rc] = 0u;
 #pragma unroll
-        for (int rj = 0; rj < CR; ++rj) {
-            uint64_t m = ballot(k[rj] != INVALID && !present[rj]);
-            while (m) {
-                const uint32_t lj = static_cast<uint32_t>(__builtin_ctzll(m));
-                m &= m - 1;
-                const uint32_t kj = readlane(k[rj], lj);
-                const uint32_t jidx = static_cast<uint32_t>(rj) * 64u + lj;
-#pragma unroll
-                for (int rc = 0; rc < CR; ++rc) {
-                    const uint32_t idx = static_cast<uint32_t>(rc) * 64u + lane;
-                    dup[rc] = dup[rc] || (k[rc] == kj && jidx < idx);
+            for (int h = 0; h < 2; ++h) {
+                const bool valid = (upper == (h == 1)) && k[rc] != INVALID;
+                if (ballot(valid) == 0) continue;
+                const bool absent = valid && !test_lane(k[rc]);
+                // first occurrence among the round's absent keys: a key equal to one of them
+                // hashes to the same bits, so it is absent too, and only absent keys can be new
+                uint64_t m = ballot(absent);
+                bool dup = false;
+                while (m) {
+                    const uint32_t lj = static_cast<uint32_t>(__builtin_ctzll(m));
+                    m &= m - 1;
+                    dup = dup || (k[rc] == readlane(k[rc], lj) && lj < lane);
                 }
+                wave_sync();  // every test of the round reads the bits before any is set
+                if (valid) set_lane(k[rc]);
+                isnew[rc] = (absent && !dup) ? 1u : isnew[rc];
+                wave_sync();
             }
         }
-        wave_sync();
-#pragma unroll
-        for (int rc = 0; rc < CR; ++rc) {
-            if (k[rc] != INVALID) set_lane(k[rc]);
-            isnew[rc] = (k[rc] != INVALID && !present[rc] && !dup[rc]) ? 1u : 0u;
-        }
-        wave_sync();
     }
 };
 
@@ -810,6 +810,52 @@ __device__ __forceinline__ uint4 load_quad(const uint32_t* codes, uint32_t nb, u
                                            const QuadShape& S) {
     const uint32_t n = nb < R ? nb : 0u;
     return *reinterpret_cast<const uint4*>(codes + static_cast<uint64_t>(n) * S.cws + 4u * qi);
+}
+
+// Narrow codes (pdim <= 128, cws = 4 words per neighbour) with one candidate register
+// (R <= 64): two lanes per neighbour, so the popcounts of a 32-neighbour row run on every
+// lane.  Lane l takes words 2 (l / 32) and 2 (l / 32) + 1 of neighbour l % 32 (and of
+// neighbour 32 + l % 32 when R > 32) in one 8-byte load; the two halves of a neighbour's
+// raw sum meet across lanes l and l + 32.  Loads are issued unconditionally (neighbours
+// >= R read neighbour 0; the caller ignores those lanes).
+struct CodeHalves {
+    uint2 a, b;
+};
+
+__device__ __forceinline__ CodeHalves load_code_halves(const uint32_t* codes, uint32_t R, const QuadShape& S) {
+    const uint32_t lane = lane_id();
+    const uint32_t nb = lane & 31u, w = 2u * (lane >> 5);
+    CodeHalves h;
+    h.a = *reinterpret_cast<const uint2*>(codes + static_cast<uint64_t>(nb < R ? nb : 0u) * S.cws + w);
+    h.b = make_uint2(0u, 0u);
+    if (R > 32u)
+        h.b = *reinterpret_cast<const uint2*>(codes + static_cast<uint64_t>(nb + 32u < R ? nb + 32u : 0u) * S.cws + w);
+    return h;
+}
+
+// raw sum of neighbour `lane` from the halves and the 24 shared plane words (planes4, LDS)
+__device__ __forceinline__ uint32_t raw_halves(const uint32_t* planes4, const CodeHalves& h, uint32_t R) {
+    const uint32_t lane = lane_id();
+    const uint32_t* pw = planes4 + 2u * (lane >> 5);
+    uint2 w[6];
+#pragma unroll
+    for (int b = 0; b < 6; ++b) w[b] = *reinterpret_cast<const uint2*>(pw + 4 * b);
+    auto half_sum = [&](uint2 c) __attribute__((always_inline)) {
+        uint32_t r = 0;
+#pragma unroll
+        for (int b = 0; b < 6; ++b) {
+            uint32_t n = static_cast<uint32_t>(__builtin_popcount(w[b].x & c.x));
+            n += static_cast<uint32_t>(__builtin_popcount(w[b].y & c.y));
+            r += n << b;
+        }
+        return r + bsw::xor_lane<32>(r);
+    };
+    uint32_t raw = half_sum(h.a);
+    if (R > 32u) {
+        const uint32_t rb = half_sum(h.b);
+        raw = lane < 32u ? raw : rb;
+    }
+    return raw;
 }
 
 // raw = sum_b 2^b * popcount(plane_b & code) over the four words of a quad

@@ -145,14 +145,18 @@ search_kernel(const SearchParams p) {
             for (int rc = 0; rc < CR; ++rc) cm[rc] = 0;
 
             // forgettable filter: clear and re-insert the beam ids (gpu_search_base.cuh:173-181)
+            // in the reference's order, its descending buffer from position 0 (largest key
+            // first).  Every beam id was admitted by the table and the table admits at most
+            // `cap` ids between resets, so the beam never holds more ids than the table
+            // accepts: the order cannot change which ids are kept.
             if (p.reset > 0 && --until_reset == 0) {
                 until_reset = p.reset;
                 if constexpr (MODE == MODE_HASH) {
                     hf.clear();
 #pragma unroll
-                    for (int r = 0; r < TR; ++r) {
+                    for (int r = TR - 1; r >= 0; --r) {
                         const uint32_t id = (beam[r] == EMPTY_KEY) ? INVALID : key_id(beam[r]);
-                        hf.insert_batch(id);
+                        hf.insert_batch<true>(id);
                     }
                 } else {
                     bf.clear();
@@ -303,18 +307,11 @@ search_kernel(const SearchParams p) {
             }
             constexpr int NC = WIDE ? 4 : CR;
             uint4 cw[NC];
-            // Narrow codes (4 words per neighbour, one candidate register): two lanes per
-            // neighbour, two words each -- lane l takes words 2 (l / 32), 2 (l / 32) + 1 of
-            // neighbour l % 32 (and of neighbour 32 + l % 32 when R > 32) -- so the popcounts
-            // of a 32-neighbour row run on every lane; lanes l and l + 32 add their halves.
+            // narrow codes with one candidate register: two lanes per neighbour (load_code_halves)
             constexpr bool HALVES = !WIDE && CR == 1;
-            uint2 ca = make_uint2(0u, 0u), cb = make_uint2(0u, 0u);
+            CodeHalves ch;
             if constexpr (HALVES) {
-                const uint32_t nb = lane & 31u, w = 2u * (lane >> 5);
-                ca = *reinterpret_cast<const uint2*>(codes + static_cast<uint64_t>(nb < p.R ? nb : 0u) * S.cws + w);
-                if (p.R > 32u)
-                    cb = *reinterpret_cast<const uint2*>(
-                        codes + static_cast<uint64_t>(nb + 32u < p.R ? nb + 32u : 0u) * S.cws + w);
+                ch = load_code_halves(codes, p.R, S);
             } else {
 #pragma unroll
                 for (int t = 0; t < NC; ++t) {
@@ -339,25 +336,7 @@ search_kernel(const SearchParams p) {
                     raw[rc] = rawbuf[i < p.R ? i : 0u];
                 }
             } else if constexpr (HALVES) {
-                const uint32_t* pw = planes4 + 2u * (lane >> 5);
-                uint2 w[6];
-#pragma unroll
-                for (int b = 0; b < 6; ++b) w[b] = *reinterpret_cast<const uint2*>(pw + 4 * b);
-                auto half_sum = [&](uint2 c) __attribute__((always_inline)) {
-                    uint32_t r = 0;
-#pragma unroll
-                    for (int b = 0; b < 6; ++b) {
-                        uint32_t n = static_cast<uint32_t>(__builtin_popcount(w[b].x & c.x));
-                        n += static_cast<uint32_t>(__builtin_popcount(w[b].y & c.y));
-                        r += n << b;
-                    }
-                    return r + bsw::xor_lane<32>(r);
-                };
-                raw[0] = half_sum(ca);
-                if (p.R > 32u) {
-                    const uint32_t rb = half_sum(cb);
-                    raw[0] = lane < 32u ? raw[0] : rb;
-                }
+                raw[0] = raw_halves(planes4, ch, p.R);
             } else {
 #pragma unroll
                 for (int b = 0; b < 6; ++b) pl[b] = reinterpret_cast<const uint4*>(planes4)[b];

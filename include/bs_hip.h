@@ -180,8 +180,10 @@ int bs_debug_l2(bs_index idx, const float* queries, uint64_t nq, const uint32_t*
                 const uint32_t* ni, uint64_t npairs, float* out);
 
 /* Quantize one query (sign flip, WHT, dithered 6-bit codes, seed) and estimate nn
- * neighbours: codes_nbr nn*(pdim/32) u32, factors 3*degree f32 (tx|fdq|fvq, nn <= 64,
- * nn <= degree).  Outputs: codes_out pdim u8, scal_out {low, width} f32, sum_q_out,
+ * neighbours: codes_nbr nn*(pdim/32) u32, factors 3*degree f32 (tx|fdq|fvq, nn <= 128,
+ * nn <= degree).  The raw sums take the search kernel's path for the layout: pdim <= 128
+ * with nn <= 64 two lanes per neighbour, pdim <= 128 with nn > 64 a neighbour per lane
+ * and register, pdim > 128 pdim/128 lanes per neighbour.  Outputs: codes_out pdim u8, scal_out {low, width} f32, sum_q_out,
  * raw_out nn u32, est_out nn f32.  Replaces RabitqQuantizer::quantize + RabitQFastScan
  * (fastscan.cuh:151-369). */
 int bs_debug_fastscan(const float* query, const float* signs, uint32_t dim, uint32_t seed,

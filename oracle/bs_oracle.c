@@ -323,11 +323,14 @@ static uint32_t hash_contains(const hashf* h, uint32_t k) {
 }
 
 /* BloomFilter (filter_bloom.cuh:13-131): 2^max(5, log2ceil(cap)) bits, k = 3 hashes.
- * The reference tests all three bits then sets them (test-then-atomicOr), so two lanes
- * inserting the same key in one step can both see "new" (a race).  Defined rule here
- * (batch semantics): for one lane-parallel batch, a key is new iff not all of its bits
- * were set before the batch and it is the first occurrence of its value in the batch;
- * then all bits of all keys of the batch are set. */
+ * The reference's warp filters a row in rounds of 32 neighbours (gpu_search_warp.cuh:203-205,
+ * lane stride BX = 32); each lane tests its key's three bits, then sets them
+ * (test-then-atomicOr, filter_bloom.cuh:104-120), so a round sees the bits of the earlier
+ * rounds, and two lanes of one round holding the same key can both see "new" (a race).
+ * Defined rule here: bloom_insert_batch is one round -- a key is new iff not all of its
+ * bits were set before the round and it is the first occurrence of its value in the
+ * round; then all bits of all keys of the round are set.  bloom_insert_rounds splits a
+ * row into rounds of 32. */
 typedef struct {
     uint32_t* w;
     uint32_t bitlen, mask, words;
@@ -394,6 +397,18 @@ static void bloom_insert_batch(bloomf* b, const uint32_t* keys, int m, uint32_t*
         if (keys[i] != ORC_INVALID_ID) bloom_set(b, keys[i]);
 }
 
+/* a row of m keys in rounds of 32 (gpu_search_warp.cuh:203-205) */
+static void bloom_insert_rounds(bloomf* b, const uint32_t* keys, int m, uint32_t* out) {
+    for (int r0 = 0; r0 < m; r0 += 32) bloom_insert_batch(b, keys + r0, (m - r0 < 32) ? m - r0 : 32, out + r0);
+}
+
+void orc_bloom_hashes(uint32_t capacity, uint32_t key, uint32_t* h) {
+    bloomf b;
+    bloom_init(&b, capacity);
+    bloom_hashes(&b, key, h);
+    bloom_free(&b);
+}
+
 static void hash_insert_batch(hashf* h, const uint32_t* keys, int m, uint32_t* out) {
     for (int i = 0; i < m; ++i) out[i] = (keys[i] == ORC_INVALID_ID) ? 0u : hash_insert(h, keys[i]);
 }
@@ -404,7 +419,7 @@ int orc_filter_run(int bloom, uint32_t capacity, const uint32_t* keys, int nbatc
         bloomf b;
         bloom_init(&b, capacity);
         for (int i = 0; i < nbatch; ++i)
-            bloom_insert_batch(&b, keys + (size_t)i * bsize, bsize, out_new + (size_t)i * bsize);
+            bloom_insert_rounds(&b, keys + (size_t)i * bsize, bsize, out_new + (size_t)i * bsize);
         for (int i = 0; i < nquery; ++i) out_contains[i] = (uint32_t)bloom_test(&b, qkeys[i]);
         bloom_free(&b);
     } else {
@@ -509,7 +524,8 @@ static void write_beam_out(const beam_t* b, uint32_t K, uint32_t* res, float* di
  *   new ones become candidates with exact L2.  A final merge catches the last
  *   candidates when the loop ran out of iterations. */
 static void search_base_gpu(const orc_index* ix, const orc_cfg* cfg, const float* q,
-                            uint32_t* res, float* dists, orc_stats* st) {
+                            uint32_t* res, float* dists, orc_stats* st, int32_t stop_iter,
+                            uint64_t* beam_snap, uint32_t* filt_snap, uint32_t* n_snap) {
     const int R = ix->degree, dim = ix->dim;
     const int bloom = cfg->mode == ORC_BASE_BLOOM;
     beam_t b;
@@ -519,15 +535,13 @@ static void search_base_gpu(const orc_index* ix, const orc_cfg* cfg, const float
     if (bloom) bloom_init(&bf, cfg->filter_capacity);
     else hash_init(&h, cfg->filter_capacity);
     uint64_t* cand = (uint64_t*)malloc(sizeof(uint64_t) * (size_t)R);
-    /* flags serve both the R-key expansion batches and the 64-key reset batches */
-    uint32_t* flags = (uint32_t*)malloc(sizeof(uint32_t) * (size_t)(R > 64 ? R : 64));
-    uint32_t* ids = (uint32_t*)malloc(sizeof(uint32_t) * (size_t)(R > 64 ? R : 64));
+    uint32_t* flags = (uint32_t*)malloc(sizeof(uint32_t) * (size_t)R);
     uint32_t nc = 0;
 
     const uint32_t ep = cfg->entry_point;
     cand[nc++] = orc_make_key(l2_of(cfg->l2_kind, q, ix->vecs + (size_t)ep * dim, dim), ep, 0);
     st->dist_evals++;
-    if (bloom) bloom_insert_batch(&bf, &ep, 1, flags);
+    if (bloom) bloom_set(&bf, ep);
     else hash_insert(&h, ep);
 
     for (int32_t iter = 0; iter < cfg->max_iterations; ++iter) {
@@ -535,23 +549,37 @@ static void search_base_gpu(const orc_index* ix, const orc_cfg* cfg, const float
         beam_merge(&b, cand, nc);
         nc = 0;
         if (cfg->reset_interval > 0 && (iter + 1) % cfg->reset_interval == 0) {
-            /* forgettable reset (gpu_search_base.cuh:173-181): re-insert the beam ids in
-             * ascending beam order, 64 at a time (one lane-parallel batch per beam row). */
+            /* forgettable reset (gpu_search_base.cuh:173-181): clear, then re-insert the beam
+             * ids walking the reference's descending buffer from position 0 (the largest key
+             * first), one at a time; a table smaller than the beam keeps the first ones. */
             if (bloom) bloom_clear(&bf);
             else hash_clear(&h);
-            for (uint32_t r0 = 0; r0 < b.T; r0 += 64) {
-                uint32_t m = (b.T - r0 < 64) ? b.T - r0 : 64;
-                for (uint32_t i = 0; i < m; ++i)
-                    ids[i] = (b.k[r0 + i] == ORC_EMPTY_KEY) ? ORC_INVALID_ID : key_id(b.k[r0 + i]);
-                if (bloom) bloom_insert_batch(&bf, ids, (int)m, flags);
-                else hash_insert_batch(&h, ids, (int)m, flags);
+            for (uint32_t i = b.T; i-- > 0;) {
+                if (b.k[i] == ORC_EMPTY_KEY) continue;
+                if (bloom) bloom_set(&bf, key_id(b.k[i]));
+                else hash_insert(&h, key_id(b.k[i]));
             }
+        }
+        if (iter == stop_iter) {
+            if (beam_snap) memcpy(beam_snap, b.k, sizeof(uint64_t) * b.T);
+            if (filt_snap) {
+                uint32_t nf = 0;
+                if (bloom) {
+                    memcpy(filt_snap, bf.w, sizeof(uint32_t) * bf.words);
+                    nf = bf.words;
+                } else {
+                    for (uint32_t s = 0; s < h.size; ++s)
+                        if (h.t[s] != ORC_INVALID_ID) filt_snap[nf++] = h.t[s];
+                }
+                if (n_snap) *n_snap = nf;
+            }
+            break;
         }
         uint32_t p = beam_pick(&b, 0);
         if (p == ORC_INVALID_ID) break;
         st->expansions++;
         const uint32_t* row = ix->edges + (size_t)p * R;
-        if (bloom) bloom_insert_batch(&bf, row, R, flags);
+        if (bloom) bloom_insert_rounds(&bf, row, R, flags);
         else hash_insert_batch(&h, row, R, flags);
         for (int i = 0; i < R; ++i) {
             if (row[i] == ORC_INVALID_ID || !flags[i]) continue;
@@ -564,10 +592,19 @@ static void search_base_gpu(const orc_index* ix, const orc_cfg* cfg, const float
     write_beam_out(&b, cfg->K, res, dists);
     free(cand);
     free(flags);
-    free(ids);
     if (bloom) bloom_free(&bf);
     else hash_free(&h);
     beam_free(&b);
+}
+
+int orc_base_state(const orc_index* ix, const orc_cfg* cfg, const float* query, int32_t stop_iter,
+                   uint64_t* beam_out, uint32_t* filter_out, uint32_t* n_filter) {
+    if (!ix || !cfg || (cfg->mode != ORC_BASE_HASH && cfg->mode != ORC_BASE_BLOOM) || stop_iter < 0) return -1;
+    orc_stats st = {0, 0, 0, 0, 0};
+    uint32_t* res = (uint32_t*)malloc(sizeof(uint32_t) * cfg->K);
+    search_base_gpu(ix, cfg, query, res, NULL, &st, stop_iter, beam_out, filter_out, n_filter);
+    free(res);
+    return 0;
 }
 
 /* cpu_search_base.hpp:22-82: seen set that never forgets, sort by (dist, node),
@@ -771,7 +808,7 @@ int orc_search(const orc_index* ix, const orc_cfg* cfg, const float* queries, ui
         float* d = dists ? dists + i * cfg->K : NULL;
         switch (cfg->mode) {
         case ORC_BASE_HASH:
-        case ORC_BASE_BLOOM: search_base_gpu(ix, cfg, q, r, d, &st); break;
+        case ORC_BASE_BLOOM: search_base_gpu(ix, cfg, q, r, d, &st, -1, NULL, NULL, NULL); break;
         case ORC_BASE_CPUREF: search_base_cpuref(ix, cfg, q, r, d, &st); break;
         case ORC_RABITQ_GPU: search_rabitq_gpu(ix, cfg, q, r, d, &st); break;
         case ORC_RABITQ_CPUREF: search_rabitq_cpuref(ix, cfg, q, r, d, &st); break;

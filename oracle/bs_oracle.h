@@ -98,10 +98,13 @@ float orc_estimate(uint32_t raw, int32_t sum_q, float width, float low,
                    float tx, float fdq, float fvq, float exact);
 
 /* ---- visit filters ---- */
-/* Runs nbatch batches of bsize lane-parallel inserts (keys == 0xFFFFFFFF are idle lanes),
- * writes the insert result per key, then answers nquery contains() queries. */
+/* Runs nbatch batches of bsize lane-parallel inserts (keys == 0xFFFFFFFF are idle lanes;
+ * a Bloom batch is inserted in rounds of 32 keys), writes the insert result per key, then
+ * answers nquery contains() queries. */
 int orc_filter_run(int bloom, uint32_t capacity, const uint32_t* keys, int nbatch, int bsize,
                    uint32_t* out_new, const uint32_t* qkeys, int nquery, uint32_t* out_contains);
+/* the three bit positions of `key` in a Bloom filter of `capacity` bits (filter_bloom.cuh:25-38) */
+void orc_bloom_hashes(uint32_t capacity, uint32_t key, uint32_t* h);
 
 /* ---- beam primitive harness ---- */
 /* topk slots; nbatch batches of bsize candidate keys merged in order; after each batch
@@ -112,6 +115,11 @@ int orc_beam_run(uint32_t topk, const uint64_t* keys, int nbatch, int bsize, int
 /* ---- searches ---- */
 int orc_search(const orc_index* idx, const orc_cfg* cfg, const float* queries, uint64_t nq,
                uint32_t* results, float* dists, orc_stats* stats);
+/* base / bwarp loop state of one query at iteration stop_iter, after that iteration's merge
+ * and reset, before its pick: beam_out[topk] keys; filter_out = the hash table's stored ids
+ * (n_filter of them, table order) or the Bloom words (n_filter words). */
+int orc_base_state(const orc_index* idx, const orc_cfg* cfg, const float* query, int32_t stop_iter,
+                   uint64_t* beam_out, uint32_t* filter_out, uint32_t* n_filter);
 
 /* ---- host pre/post steps (src/gpu_cli.cu:28-83) ---- */
 uint32_t orc_entry_point(const float* vecs, uint64_t n, int dim);

@@ -59,6 +59,8 @@ def lib():
             "orc_raw_dot": (u32, [vp, vp, C.c_int]),
             "orc_estimate": (f32, [u32, i32, f32, f32, f32, f32, f32, f32]),
             "orc_filter_run": (C.c_int, [C.c_int, u32, vp, C.c_int, C.c_int, vp, vp, C.c_int, vp]),
+            "orc_bloom_hashes": (None, [u32, u32, vp]),
+            "orc_base_state": (C.c_int, [C.POINTER(Index), C.POINTER(Cfg), vp, i32, vp, vp, vp]),
             "orc_beam_run": (C.c_int, [u32, vp, C.c_int, C.c_int, C.c_int, C.c_int, vp, vp]),
             "orc_search": (C.c_int, [C.POINTER(Index), C.POINTER(Cfg), vp, u64, vp, vp, vp]),
             "orc_entry_point": (u32, [vp, u64, C.c_int]),
@@ -121,6 +123,12 @@ def filter_run(bloom, capacity, keys, qkeys):
     return out_new, out_c
 
 
+def bloom_hashes(capacity, key):
+    h = np.empty(3, np.uint32)
+    lib().orc_bloom_hashes(capacity, key, _p(h))
+    return [int(x) for x in h]
+
+
 def beam_run(topk, keys, picks, pick_run):
     keys = np.ascontiguousarray(keys, np.uint64)
     nb, bs = keys.shape
@@ -158,6 +166,19 @@ class OracleIndex:
         stats = np.array([[s.iterations, s.expansions, s.dist_evals, s.est_evals, s.rerank_evals] for s in st],
                          dtype=np.uint64).reshape(nq, 5)
         return res, d, stats
+
+
+    def base_state(self, query, mode, topk, entry, cap, reset, stop_iter, K=10, max_it=1024, l2=L2_WAVE):
+        """beam keys and filter contents of one base/bwarp query after iteration stop_iter's
+        merge and reset (hash: the stored ids; Bloom: the bit words)"""
+        q = np.ascontiguousarray(query, np.float32)
+        c = Cfg(mode, l2, K, topk, cap, entry, max_it, reset)
+        beam = np.full(topk, EMPTY_KEY, np.uint64)
+        filt = np.empty(max(cap, 32) * 2, np.uint32)
+        nf = C.c_uint32(0)
+        if lib().orc_base_state(C.byref(self.ix), C.byref(c), _p(q), stop_iter, _p(beam), _p(filt), C.byref(nf)) != 0:
+            raise ValueError("orc_base_state failed")
+        return beam, filt[: nf.value].copy()
 
 
 def entry_point(vecs):

@@ -73,3 +73,62 @@ def load_cpucli(name):
 @pytest.fixture(scope="session")
 def golden_sets():
     return {n: load_cpucli(n) for n in ("d32", "d100")}
+
+
+TREE_SETS = ("d32r8", "d100r16", "d64r48")
+
+
+def load_rqtree(name):
+    """the RaBitQ special case where the GPU search and the reference cpu_cli agree id for id
+    (tests/golden/make_golden.py, rqtree_*)"""
+    z = np.load(os.path.join(GOLDEN, f"rqtree_{name}.npz"), allow_pickle=False)
+    meta = json.load(open(os.path.join(GOLDEN, f"rqtree_{name}.json")))
+    return {k: z[k] for k in z.files}, meta
+
+
+# ---------------------------------------------------------------------------------------
+# Bloom filter restated from the reference (filter_bloom.cuh:25-38,104-120 and the row loop
+# of gpu_search_warp.cuh:203-205) in Python integers, independent of the oracle and the kernel
+# ---------------------------------------------------------------------------------------
+INVALID_ID = 0xFFFFFFFF
+_M32 = 0xFFFFFFFF
+
+
+def _mix(x):
+    # filter_bloom.cuh:25-38: x ^= x >> 16; x *= 0x45d9f3b; x ^= x >> 16 (32-bit arithmetic)
+    x ^= x >> 16
+    x = (x * 0x45D9F3B) & _M32
+    return x ^ (x >> 16)
+
+
+def bloom_bits(key, cap):
+    b = max(5, (cap - 1).bit_length())
+    mask = (1 << b) - 1
+    return [_mix(key) & mask, _mix((key * 0x9E3779B9) & _M32) & mask, _mix((key * 0x517CC1B7) & _M32) & mask]
+
+
+def bloom_simulate(cap, batches):
+    """the reference's row filter (gpu_search_warp.cuh:203-205 with filter_bloom.cuh:104-120):
+    rounds of 32 consecutive keys; each round tests against the bits of all earlier rounds,
+    then sets its keys' bits; a key held twice in one round is new once (first index)"""
+    bitset = set()
+    new = np.zeros(batches.shape, np.uint32)
+    for b in range(batches.shape[0]):
+        row = [int(k) for k in batches[b]]
+        for r0 in range(0, len(row), 32):
+            seen_absent = set()
+            for i in range(r0, min(r0 + 32, len(row))):
+                k = row[i]
+                if k == INVALID_ID:
+                    continue
+                absent = not all(h in bitset for h in bloom_bits(k, cap))
+                if absent and k not in seen_absent:
+                    new[b, i] = 1
+                if absent:
+                    seen_absent.add(k)
+            for i in range(r0, min(r0 + 32, len(row))):
+                if row[i] != INVALID_ID:
+                    bitset.update(bloom_bits(row[i], cap))
+    return new, bitset
+
+

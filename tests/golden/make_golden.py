@@ -13,8 +13,17 @@ host library.  The fixtures hold only data: inputs and the reference's outputs.
                         are given as its ground truth (every id of every query agrees).
   build_<name>.json     sha256 of the reference build_graph / build_rabitq output files
                         for generator parameters (checks the host builders without _ref).
+  rqtree_<name>.npz     the case where the GPU RaBitQ search (gpu_search_rabitq.cuh:191-340)
+                        and the reference cpu_cli rabitq search (cpu_search_rabitq.hpp:115-150)
+                        must return the same ids: every edge has fdq = fvq = 0, so both
+                        estimators give tx + exact(parent) whatever the query codes; the graph
+                        is a tree padded with self-loops, so no node is reached from two
+                        parents and neither the expanded-set re-entry nor the dedup flush of
+                        the GPU search can act; vectors are small integers, so every L2 sum is
+                        exact in any order.  Inputs plus the ids of the CPU oracle, accepted
+                        only if the reference cpu_cli scores them at recall exactly 1.
 
-usage: python tests/golden/make_golden.py
+usage: python tests/golden/make_golden.py [all|tree]
 """
 import hashlib
 import json
@@ -67,7 +76,90 @@ def run_cli(cfg):
     return out
 
 
+# name: n, dim, degree, nq, seed
+TREES = {
+    "d32r8": dict(n=2000, dim=32, degree=8, nq=48, seed=71),
+    "d100r16": dict(n=1500, dim=100, degree=16, nq=48, seed=72),
+    "d64r48": dict(n=1200, dim=64, degree=48, nq=48, seed=73),
+}
+TREE_SEARCH = [(10, 32, 1024), (10, 64, 1024), (20, 128, 1024), (10, 64, 40)]  # K, topk, max_iterations
+
+
+def make_tree(spec):
+    """random recursive tree: node perm[i] hangs under a random earlier node with a free
+    slot; rows list the children in random slots and pad with the node's own id"""
+    rng = np.random.default_rng(spec["seed"])
+    n, R = spec["n"], spec["degree"]
+    perm = rng.permutation(n)
+    edges = np.repeat(np.arange(n, dtype=np.uint32)[:, None], R, axis=1)
+    nchild = np.zeros(n, np.int64)
+    free = [int(perm[0])]
+    for i in range(1, n):
+        j = int(rng.integers(0, len(free)))
+        par = free[j]
+        edges[par, nchild[par]] = perm[i]
+        nchild[par] += 1
+        if nchild[par] == R:
+            free[j] = free[-1]
+            free.pop()
+        free.append(int(perm[i]))
+    for u in range(n):
+        rng.shuffle(edges[u])
+    return edges, int(perm[0])
+
+
+def make_trees():
+    for name, spec in TREES.items():
+        rng = np.random.default_rng(spec["seed"] + 1000)
+        n, dim, R, nq = spec["n"], spec["dim"], spec["degree"], spec["nq"]
+        base = rng.integers(0, 8, (n, dim)).astype(np.float32)
+        qs = rng.integers(0, 8, (nq, dim)).astype(np.float32)
+        edges, root = make_tree(spec)
+        pdim = host.padded_dim(dim)
+        codes = rng.integers(0, 2**32, (n, R * (pdim // 32)), dtype=np.uint64).astype(np.uint32)
+        factors = np.zeros((n, 3 * R), np.float32)
+        factors[:, :R] = rng.uniform(0.0, 40.0, (n, R)).astype(np.float32)
+        factors[:, :R][rng.random((n, R)) < 0.05] = np.finfo(np.float32).max  # tx = FLT_MAX edges
+        signs = np.where(rng.random(pdim) < 0.5, -1.0, 1.0).astype(np.float32) / np.float32(np.sqrt(pdim))
+        d = tempfile.mkdtemp()
+        host.write_fvecs(f"{d}/base.fvecs", base)
+        host.write_fvecs(f"{d}/q.fvecs", qs)
+        host.write_graph(f"{d}/g.bin", edges)
+        host.write_codebook(f"{d}/cb.bin", base, edges, root, codes, factors, signs)
+        oi = po.OracleIndex(base, edges, codes, factors, signs)
+        arrays = dict(base=base, queries=qs, edges=edges, codes=codes, factors=factors, signs=signs,
+                      entry=np.int64(root))
+        meta = {"spec": spec, "searches": []}
+        for K, topk, max_it in TREE_SEARCH:
+            ids, dists, st = oi.search(qs, K, po.RABITQ_GPU, topk, root, max_it, 4096, 0, po.L2_WAVE)
+            cids, cd, _ = oi.search(qs, K, po.RABITQ_CPUREF, topk, root, max_it, 4096, 0, po.L2_SEQ)
+            if not (np.array_equal(ids, cids) and np.array_equal(dists, cd)):
+                raise SystemExit(f"{name}: the two oracle searches differ on a tree")
+            if (ids == po.INVALID_ID).any():
+                raise SystemExit(f"{name}: fewer than K results")
+            host.write_ivecs(f"{d}/gt_oracle.ivecs", ids.astype(np.int32))
+            cfg = {"data": {"graph": f"{d}/g.bin", "base": f"{d}/base.fvecs", "query": f"{d}/q.fvecs",
+                            "gt": f"{d}/gt_oracle.ivecs", "codebook": f"{d}/cb.bin"},
+                   "search": {"mode": "rabitq", "K": K, "topk_size": topk, "max_iterations": max_it}}
+            agree = run_cli(cfg)
+            if agree["recall"] != 1.0:
+                raise SystemExit(f"tree {name} K={K} topk={topk}: reference cpu_cli disagrees ({agree['recall']})")
+            key = f"ids_k{K}_t{topk}_m{max_it}"
+            arrays[key] = ids
+            arrays["dists_" + key[4:]] = dists
+            meta["searches"].append({"K": K, "topk": topk, "max_iterations": max_it, "key": key,
+                                     "expansions_per_query": float(st[:, 1].mean()), "ref_recall_vs_ids": 1.0})
+        np.savez_compressed(os.path.join(HERE, f"rqtree_{name}.npz"), **arrays)
+        with open(os.path.join(HERE, f"rqtree_{name}.json"), "w") as f:
+            json.dump(meta, f, indent=1)
+        print("tree", name, "ok", meta["searches"])
+
+
 def main():
+    if len(sys.argv) > 1 and sys.argv[1] == "tree":
+        make_trees()
+        return
+    make_trees()
     for seed in (42, 123):
         with open(os.path.join(HERE, f"fastscan_s{seed}.bin"), "wb") as f:
             f.write(subprocess.run([os.path.join(REF, "ref_fastscan"), str(seed), "48"], capture_output=True,

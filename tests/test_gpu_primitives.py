@@ -4,7 +4,7 @@ test_topk_*_merge.cu, *_no_dup.cu, test_topk_reg_pick_order.cu, *_bitonic_sort*.
 import numpy as np
 import pytest
 
-from conftest import load_fastscan_golden
+from conftest import bloom_bits, bloom_simulate, load_fastscan_golden
 from beam_search_collab_amd import host, search
 from oracle import pyoracle as po
 
@@ -22,6 +22,29 @@ def test_fastscan_matches_reference_golden(gpu, seed):
         assert sq == r["sum_q"]
         assert np.array_equal(raw, r["raw"])
         assert est.tobytes() == r["est"].tobytes(), (r["dim"], est, r["est"])
+
+
+@pytest.mark.parametrize("dim", [20, 64, 100, 128, 200, 960])
+@pytest.mark.parametrize("nn", [1, 8, 31, 32, 33, 48, 64, 65, 100, 128])
+def test_fastscan_kernel_paths_against_oracle(gpu, dim, nn):
+    """every raw-sum path of the search kernel (two lanes per neighbour for narrow codes and
+    up to 64 neighbours, including the second half-register past 32; a neighbour per lane
+    beyond 64; the wide layout) against the oracle's closed form raw = sum of selected codes"""
+    rng = np.random.default_rng(dim * 1000 + nn)
+    pdim = host.padded_dim(dim)
+    wpp = pdim // 32
+    q = rng.standard_normal(dim).astype(np.float32)
+    signs = np.where(rng.random(pdim) < 0.5, -1, 1).astype(np.float32) / np.float32(np.sqrt(pdim))
+    nbr = rng.integers(0, 2**32, (nn, wpp), dtype=np.uint64).astype(np.uint32)
+    fac = rng.standard_normal(3 * nn).astype(np.float32)
+    codes, low, width, sq, raw, est = search.debug_fastscan(q, signs, dim, 0, nbr, fac, nn, nn, np.float32(3.5))
+    ocodes, olow, owidth, osq = po.quantize(q, signs, dim, 0)
+    assert np.array_equal(codes, ocodes)
+    assert sq == osq
+    for j in range(nn):
+        assert raw[j] == po.raw_dot(ocodes, nbr[j], pdim), (dim, nn, j)
+        want = po.estimate(int(raw[j]), osq, owidth, olow, fac[j], fac[nn + j], fac[2 * nn + j], 3.5)
+        assert np.float32(est[j]).tobytes() == np.float32(want).tobytes()
 
 
 @pytest.mark.parametrize("dim", [1, 3, 16, 25, 32, 100, 128, 200, 384, 960, 1024])
@@ -121,6 +144,23 @@ def test_filters_match_oracle(gpu, bloom, cap):
     onew, ocont = po.filter_run(bloom, cap, keys, qk)
     assert np.array_equal(new, onew)
     assert np.array_equal(cont, ocont)
+
+
+@pytest.mark.parametrize("cap", [32, 64, 256, 1024])
+def test_bloom_filter_bits_and_rounds(gpu, cap):
+    """the device Bloom filter against the reference's rule restated in Python integers
+    (conftest.bloom_simulate: three mixer hashes, rows filtered in rounds of 32 keys): which
+    keys are new, and contains() for keys whose bits are or are not all set"""
+    rng = np.random.default_rng(cap)
+    keys = rng.integers(0, 3 * cap, (12, 64)).astype(np.uint32)
+    keys[:, 50:] = 0xFFFFFFFF
+    keys[2, 33] = keys[2, 5]   # same key in both rounds
+    keys[3, 9] = keys[3, 4]    # same key twice in one round
+    qk = rng.integers(0, 3 * cap, 400).astype(np.uint32)
+    want_new, bitset = bloom_simulate(cap, keys)
+    new, cont = search.debug_filter(1, cap, keys, qk)
+    assert np.array_equal(new, want_new)
+    assert cont.tolist() == [int(all(h in bitset for h in bloom_bits(int(k), cap))) for k in qk]
 
 
 def test_host_tools_do_not_need_the_gpu_but_index_does(gpu):

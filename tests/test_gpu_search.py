@@ -233,3 +233,67 @@ def test_recall_parity_with_cpu_reference(gpu):
         # the GPU estimator (dithered quantizer, expanded-set re-entry) is not the CPU one
         # (gpu_search_rabitq.cuh vs cpu_search_rabitq.hpp): it may only be better
         assert rg >= rq - 0.005, (topk, rg, rq)
+
+
+# ---------------------------------------------------------------------------------------
+# cases the benchmarked configurations run
+# ---------------------------------------------------------------------------------------
+@pytest.mark.parametrize("mode", ["base", "warp2", "bwarp1", "rabitq"])
+@pytest.mark.parametrize("topk", [256, 512])
+def test_k100_flush_across_registers(gpu, mode, topk):
+    """K = 100 (configs B, C, E): the flush spans two beam registers"""
+    ds = dataset(4000, 128, 32, 64)
+    assert_same(*run_both(ds, mode, 100, topk), f"{mode} topk={topk} K=100")
+
+
+@pytest.mark.parametrize("nq", [400, 800])
+def test_config_e_shape(gpu, nq):
+    """config E settings on a small base: d960, degree 32, topk 256, K 100; base mode with 400
+    and 800 queries takes the 4- and the 2-wavefront split (slots = resident wavefronts of
+    the 8-pass instance x CUs), rabitq the wide-code path (pdim 1024)"""
+    ds = dataset(1500, 960, 32, nq)
+    for mode in ("base", "rabitq"):
+        assert_same(*run_both(ds, mode, 100, 256), f"{mode} d960 nq={nq}")
+
+
+@pytest.mark.parametrize("mode", ["warp1", "bwarp2", "rabitq"])
+@pytest.mark.parametrize("topk", [128, 256])
+def test_degree_100_two_candidate_registers(gpu, mode, topk):
+    """degree > 64 (two candidate registers) with beams of two and four registers; the Bloom
+    filter's four 32-key rounds; cap 1024 at reset 16 makes Bloom false positives common"""
+    ds = dataset(2500, 64, 100, 40, "normalized")
+    assert_same(*run_both(ds, mode, 10, topk), f"{mode} R=100 topk={topk}")
+
+
+@pytest.mark.parametrize("degree", [48, 64, 100])
+@pytest.mark.parametrize("ny", [1, 4])
+def test_bloom_rounds_small_filters(gpu, degree, ny):
+    """bwarp at degree 48, 64 and 100 with small Bloom filters (many false positives): the
+    rounds of 32 neighbours decide which keys are new"""
+    ds = dataset(2500, 64, degree, 40, "normalized")
+    for cap, reset in ((256, 2), (1024, 8)):
+        assert_same(*run_both(ds, "bwarp", 10, 128, cap=cap, reset=reset, ny=ny),
+                    f"bwarp{ny} R={degree} cap={cap}")
+
+
+# ---------------------------------------------------------------------------------------
+# the RaBitQ trajectory against the reference cpu_cli where the two coincide
+# ---------------------------------------------------------------------------------------
+from conftest import TREE_SETS, load_rqtree  # noqa: E402
+
+
+@pytest.mark.parametrize("name", TREE_SETS)
+def test_rabitq_trees_match_reference_cpu_cli(gpu, name):
+    """tests/golden/rqtree_*: fdq = fvq = 0, a tree padded with self-loops, integer vectors --
+    the reference cpu_cli rabitq search returns these ids (it scored them at recall 1 as its
+    own ground truth); the GPU search must return the same ids, order and exact distances"""
+    arrays, meta = load_rqtree(name)
+    g = search.GPUGraph(arrays["base"], arrays["edges"])
+    g.attach_rabitq(arrays["codes"], arrays["factors"], arrays["signs"])
+    ep = int(arrays["entry"])
+    for s in meta["searches"]:
+        cfg = GPURabitqSearchCfg(s["topk"], 4096, ep, s["max_iterations"])
+        ids, d, st = g.search(arrays["queries"], s["K"], "rabitq", cfg, with_dists=True)
+        assert np.array_equal(ids, arrays[s["key"]]), (name, s)
+        assert d.tobytes() == arrays["dists_" + s["key"][4:]].tobytes(), (name, s)
+        assert abs(st["expansions"] / arrays["queries"].shape[0] - s["expansions_per_query"]) < 1e-9

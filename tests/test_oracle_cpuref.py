@@ -62,3 +62,56 @@ def test_cpuref_live_against_reference_binary(dim, degree, topk):
                              text=True, check=True).stdout
         line = [x for x in out.splitlines() if x.startswith("recall@")][0]
         assert float(line.split(":")[1]) == 1.0, (mode, out)
+
+
+# ---------------------------------------------------------------------------------------
+# The GPU RaBitQ trajectory against the reference cpu_cli where the two must coincide
+# ---------------------------------------------------------------------------------------
+from conftest import TREE_SETS, load_rqtree  # noqa: E402
+
+
+@pytest.mark.parametrize("name", TREE_SETS)
+def test_rabitq_gpu_semantics_match_cpu_cli_on_trees(name):
+    """fdq = fvq = 0 makes both estimators tx + exact(parent); a tree padded with self-loops
+    reaches every node from one parent only, so the GPU search's expanded-set re-entry and
+    dedup flush (gpu_search_rabitq.cuh:249-273,319-339) cannot act; integer vectors make
+    every L2 exact.  The GPU-semantics oracle must then return the reference cpu_cli's ids
+    (cpu_search_rabitq.hpp:115-150), distances and order."""
+    arrays, meta = load_rqtree(name)
+    oi = po.OracleIndex(arrays["base"], arrays["edges"], arrays["codes"], arrays["factors"], arrays["signs"])
+    ep = int(arrays["entry"])
+    for s in meta["searches"]:
+        ids, d, st = oi.search(arrays["queries"], s["K"], po.RABITQ_GPU, s["topk"], ep, s["max_iterations"], 4096,
+                               0, po.L2_WAVE)
+        assert np.array_equal(ids, arrays[s["key"]]), (name, s)
+        assert np.array_equal(d, arrays["dists_" + s["key"][4:]]), (name, s)
+        assert abs(st[:, 1].mean() - s["expansions_per_query"]) < 1e-9
+        # no picked node was expanded before (no re-entry): every iteration expands, but the
+        # last one of a search that ran out of unexpanded entries
+        assert np.all((st[:, 0] - st[:, 1] == 0) | (st[:, 0] - st[:, 1] == 1))
+        # distances are the exact integer L2 of the returned rows
+        q, base = arrays["queries"], arrays["base"]
+        want = ((q[:, None, :].astype(np.int64) - base[ids].astype(np.int64)) ** 2).sum(-1)
+        assert np.array_equal(d.astype(np.int64), want)
+
+
+@pytest.mark.skipif(not os.path.exists(os.path.join(po.REF_DIR, "cpu_cli")), reason="reference not built here")
+@pytest.mark.parametrize("name", TREE_SETS)
+def test_rabitq_tree_fixture_live_against_reference_binary(name):
+    arrays, meta = load_rqtree(name)
+    d = tempfile.mkdtemp()
+    host.write_fvecs(f"{d}/b.fvecs", arrays["base"])
+    host.write_fvecs(f"{d}/q.fvecs", arrays["queries"])
+    host.write_graph(f"{d}/g.bin", arrays["edges"])
+    host.write_codebook(f"{d}/cb.bin", arrays["base"], arrays["edges"], int(arrays["entry"]), arrays["codes"],
+                        arrays["factors"], arrays["signs"])
+    for s in meta["searches"]:
+        host.write_ivecs(f"{d}/gt.ivecs", arrays[s["key"]].astype(np.int32))
+        cfg = {"data": {"graph": f"{d}/g.bin", "base": f"{d}/b.fvecs", "query": f"{d}/q.fvecs", "gt": f"{d}/gt.ivecs",
+                        "codebook": f"{d}/cb.bin"},
+               "search": {"mode": "rabitq", "K": s["K"], "topk_size": s["topk"],
+                          "max_iterations": s["max_iterations"]}}
+        out = subprocess.run([os.path.join(po.REF_DIR, "cpu_cli")], input=json.dumps(cfg), capture_output=True,
+                             text=True, check=True).stdout
+        line = [x for x in out.splitlines() if x.startswith("recall@")][0]
+        assert float(line.split(":")[1]) == 1.0, (name, s, out)

@@ -3,6 +3,7 @@ reference-pinned CPU-reference oracle and closed forms."""
 import numpy as np
 import pytest
 
+from conftest import bloom_bits, bloom_simulate
 from oracle import pyoracle as po
 
 
@@ -149,3 +150,106 @@ def make(d, ids):
     b = np.asarray(d, np.float32).view(np.uint32).astype(np.uint64)
     o = np.where((b & 0x80000000) != 0, (~b) & 0xFFFFFFFF, b | 0x80000000)
     return (o << np.uint64(32)) | (np.asarray(ids, np.uint64) << np.uint64(1))
+
+
+# ---------------------------------------------------------------------------------------
+# Bloom filter: bit positions and the reference's 32-lane insert rounds
+# ---------------------------------------------------------------------------------------
+# (key, h0, h1, h2) for a table of 2^22 bits; h0 of key 1 by hand: 0x45d9f3b ^ (0x45d9f3b >> 16)
+# = 0x45d9b66, & 0x3fffff = 0x1d9b66 = 1940326
+BLOOM_KNOWN = [(0, 0, 0, 0), (1, 1940326, 592371, 2267307), (2, 3880653, 1602092, 2252271),
+               (7, 1000466, 1850261, 2128728), (12345, 3342992, 830435, 3788539),
+               (1000000, 2525523, 1370009, 225021), (0xDEADBEEF, 3681678, 1963830, 596569)]
+
+
+def test_bloom_hash_positions():
+    for key, *h in BLOOM_KNOWN:
+        assert bloom_bits(key, 1 << 22) == h
+        assert po.bloom_hashes(1 << 22, key) == h
+    rng = np.random.default_rng(11)
+    for cap in (1, 32, 33, 1000, 1024, 8192, 1 << 20):
+        for key in rng.integers(0, 2**32 - 1, 200).tolist() + [0, 1, 2**31 - 1]:
+            assert po.bloom_hashes(cap, key) == bloom_bits(key, cap), (cap, key)
+
+
+def bloom_round_pair(cap, rng):
+    """keys a != b with bits(b) a subset of bits(a): b is new in a's round, not in a later one"""
+    while True:
+        a, b = (int(x) for x in rng.integers(0, 10**6, 2))
+        if a != b and set(bloom_bits(b, cap)) <= set(bloom_bits(a, cap)):
+            return a, b
+
+
+def test_bloom_rounds_of_32():
+    rng = np.random.default_rng(5)
+    a, b = bloom_round_pair(32, rng)
+    keys = np.full((1, 64), po.INVALID_ID, np.uint32)
+    keys[0, 3], keys[0, 40] = a, b           # b in the second round: a's bits are set by then
+    new, _ = po.filter_run(True, 32, keys, np.array([b], np.uint32))
+    assert new[0, 3] == 1 and new[0, 40] == 0
+    keys[0, 40], keys[0, 9] = po.INVALID_ID, b  # same round: tested before a's bits are set
+    new, _ = po.filter_run(True, 32, keys, np.array([b], np.uint32))
+    assert new[0, 3] == 1 and new[0, 9] == 1
+    # random rows of 64 keys (two rounds) on small tables, where false positives are common
+    for cap in (32, 64, 256, 1024):
+        keys = rng.integers(0, 3 * cap, (12, 64)).astype(np.uint32)
+        keys[:, 50:] = po.INVALID_ID
+        keys[2, 33] = keys[2, 5]
+        qk = rng.integers(0, 3 * cap, 200).astype(np.uint32)
+        want_new, bitset = bloom_simulate(cap, keys)
+        new, cont = po.filter_run(True, cap, keys, qk)
+        assert np.array_equal(new, want_new), cap
+        assert cont.tolist() == [int(all(h in bitset for h in bloom_bits(int(k), cap))) for k in qk]
+
+
+# ---------------------------------------------------------------------------------------
+# forgettable hash filter: resets without overflow, the re-fill order
+# ---------------------------------------------------------------------------------------
+@pytest.mark.parametrize("name", ["d32", "d100"])
+def test_base_hash_resets_without_overflow_equal_cpuref(golden_sets, name):
+    """gpu_search_base.cuh:174-181: after a reset the table holds the beam ids; a node it
+    forgot was evicted from (or never entered) a beam that keeps the T smallest keys merged
+    so far, so its second evaluation is dropped again.  With a table that cannot fill between
+    resets (capacity >= T + reset * R) the search therefore returns exactly what the CPU
+    reference (never forgets) returns, at the cost of extra distance evaluations."""
+    arrays, _ = golden_sets[name]
+    oi = _idx(arrays)
+    ep = int(arrays["entry"])
+    R = arrays["edges"].shape[1]
+    q = arrays["queries"]
+    for topk in (32, 64, 128):
+        ref, dref, sref = oi.search(q, 10, po.BASE_CPUREF, topk, ep, 1024, 1 << 16, 0)
+        for reset in (1, 4, 16):
+            cap = 1 << int(np.ceil(np.log2(topk + reset * R)))
+            ids, d, st = oi.search(q, 10, po.BASE_HASH, topk, ep, 1024, cap, reset)
+            assert np.array_equal(ids, ref), (topk, reset)
+            assert np.array_equal(d, dref), (topk, reset)
+            assert np.array_equal(st[:, 1], sref[:, 1])  # same expansions
+            assert np.all(st[:, 2] >= sref[:, 2])        # re-evaluations of forgotten nodes
+            assert st[:, 2].sum() > sref[:, 2].sum()
+
+
+def test_reset_refill_holds_beam_ids(golden_sets):
+    """gpu_search_base.cuh:174-181: at a reset the table is cleared and the beam ids are
+    re-inserted, walking the descending buffer from position 0 (largest key first).  Every
+    beam entry was admitted by the table, and between resets the table admits at most
+    `capacity` ids counting the re-inserted ones, so the beam never holds more ids than the
+    table accepts: after every reset the table holds exactly the beam ids, whatever the
+    re-insertion order (which therefore never changes a result)."""
+    arrays, _ = golden_sets["d32"]
+    oi = _idx(arrays)
+    ep = int(arrays["entry"])
+    for qi in range(4):
+        q = arrays["queries"][qi]
+        for topk, cap, reset in ((64, 1024, 4), (64, 64, 4), (128, 32, 16), (128, 64, 8), (256, 128, 1)):
+            checked = 0
+            for stop in range(reset - 1, 200, reset):
+                beam, filt = oi.base_state(q, po.BASE_HASH, topk, ep, cap, reset, stop)
+                valid = beam[beam != po.EMPTY_KEY]
+                ids = ((valid >> np.uint64(1)) & np.uint64(0x7FFFFFFF)).astype(np.int64)
+                if len(ids) == 0:
+                    continue  # the search ended before this iteration: no snapshot
+                assert len(ids) <= cap
+                assert sorted(filt.tolist()) == sorted(ids.tolist()), (qi, topk, cap, reset, stop)
+                checked += 1
+            assert checked > 0
