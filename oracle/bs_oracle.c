@@ -11,25 +11,25 @@
  *       golden vectors written by the reference's own host functions
  *       (unittest/test_fastscan.cu:54-145, compiled into oracle/_ref/ref_fastscan),
  *       committed under tests/golden/fastscan_*.bin; plus closed forms (raw sum is the
- *       integer sum of selected codes; WHT applied twice is pdim * identity).
+ *       integer sum of selected codes; codes follow the Sylvester-Hadamard rotation).
  *   orc_l2_seq       reference cpu_cli ids (bit-exact) through ORC_BASE_CPUREF.
  *   orc_l2_wave      fp64 sum within 1e-5 relative; exact on integer-valued inputs
  *                    (every partial sum is an exactly representable integer).
  *   ORC_BASE_CPUREF, ORC_RABITQ_CPUREF
  *                    result ids of the reference cpu_cli (oracle/_ref/cpu_cli) on
  *                    synthetic sets, committed under tests/golden/cpucli_*.npz.
- *   ORC_BASE_HASH    reduces to ORC_BASE_CPUREF exactly when reset_interval never
- *                    fires and the table cannot overflow (same L2 kind); the reset rule
- *                    (gpu_search_base.cuh:173-181) is checked by the invariant "after a
- *                    reset the filter holds exactly the beam ids".
- *   ORC_BASE_BLOOM   reduces to ORC_BASE_HASH when the Bloom filter has no false
- *                    positives for the keys seen (checked on small inputs by brute force);
- *                    the three hash functions are checked against hand-computed values.
- *   ORC_RABITQ_GPU   components pinned as above (quantizer, estimate, L2, rerank sort,
- *                    dedup); the trajectory itself (expanded-set re-entry,
- *                    gpu_search_rabitq.cuh:229-312) has no runnable reference here
- *                    (the reference GPU code needs CUDA): "parity unpinned" for the
- *                    trajectory, recall-only agreement with ORC_RABITQ_CPUREF.
+ *   ORC_BASE_HASH    equals ORC_BASE_CPUREF (ids, distances, expansions) when the table
+ *                    cannot fill between resets, with reset_interval 0, 1, 4 and 16
+ *                    (tests/test_oracle_semantics.py); after every reset the table holds
+ *                    exactly the beam ids (orc_base_state snapshots).
+ *   ORC_BASE_BLOOM   bit positions against hand-computed values and a Python restatement of
+ *                    filter_bloom.cuh:25-38; the 32-key round rule against that restatement
+ *                    and a closed-form pair (a key whose bits an earlier round set is not
+ *                    new); reduces to ORC_BASE_HASH when the filter has no false positives.
+ *   ORC_RABITQ_GPU   ids, order and distances of the reference cpu_cli rabitq search on the
+ *                    inputs where the two searches must coincide (fdq = fvq = 0, a tree padded
+ *                    with self-loops, integer vectors; tests/golden/rqtree_*); properties
+ *                    (exact rerank, sorted, deduplicated) and recall elsewhere.
  *   orc_entry_point  reference cpu_cli "entry=" line (bit-exact id).
  *   orc_beam_run, orc_filter_run
  *                    closed forms of the reference unit tests (shuffled 0..n-1 keep the

@@ -76,3 +76,21 @@ def test_dither_hash_is_the_reference_mixer():
     for a, b in [(0, 0), (0, 1), (0, 127), (12345, 7), (0xFFFFFFFF, 3)]:
         assert po.lib().orc_dither_hash(a, b) == mix(a, b)
     assert po.lib().orc_dither_hash(0, 0) == 0
+
+
+def test_l2_orders_against_fp64_and_integers():
+    """orc_l2_wave (the kernels' lane order) and orc_l2_seq (the reference CPU's sequential
+    sum): within 1e-5 relative of an fp64 sum, and exact when every partial sum is an
+    integer below 2^24 (then every order gives the same float)"""
+    rng = np.random.default_rng(4)
+    for dim in (1, 3, 16, 25, 32, 100, 128, 200, 384, 960, 1024):
+        for _ in range(20):
+            a = rng.standard_normal(dim).astype(np.float32) * 10
+            b = rng.standard_normal(dim).astype(np.float32) * 10
+            want = float(((a.astype(np.float64) - b.astype(np.float64)) ** 2).sum())
+            assert abs(po.l2_wave(a, b) - want) <= 1e-5 * want
+            assert abs(po.l2_seq(a, b) - want) <= 1e-5 * want
+            ai = rng.integers(0, 16, dim).astype(np.float32)
+            bi = rng.integers(0, 16, dim).astype(np.float32)
+            exact = int(((ai.astype(np.int64) - bi.astype(np.int64)) ** 2).sum())
+            assert po.l2_wave(ai, bi) == exact and po.l2_seq(ai, bi) == exact
