@@ -55,6 +55,7 @@ HIP_API = {
     "bs_index_attach_rabitq": (C.c_int, [vp, vp, vp, vp, u32]),
     "bs_search": (C.c_int, [vp, P(SearchCfg), vp, u64, vp, vp, P(Stats)]),
     "bs_search_device": (C.c_int, [vp, P(SearchCfg), vp, u64, vp, vp, vp, vp, C.c_int, P(Stats)]),
+    "bs_search_device_noalloc": (C.c_int, [vp, P(SearchCfg), vp, u64, vp, vp, vp, vp]),
     "bs_index_info": (C.c_int, [vp, P(u64), P(u32), P(u32), P(u32), P(C.c_int)]),
     "bs_index_destroy": (None, [vp]),
     "bs_index_set_query_order": (C.c_int, [vp, C.c_int]),

@@ -11,6 +11,7 @@
 #include <cstdio>
 #include <cstring>
 #include <exception>
+#include <mutex>
 #include <new>
 #include <string>
 #include <vector>
@@ -504,11 +505,13 @@ hipError_t launch(const Plan& pl, hipStream_t s) {
 }
 
 // The search in launches of at most ORDER_CHUNK queries, each preceded by the query
-// scheduling kernels that fill its launch map.
-hipError_t launch_ordered(bs_index ix, Plan pl, uint64_t nq, hipStream_t s) {
+// scheduling kernels that fill its launch map in `ows` (key[ORDER_CHUNK] | qmap[ORDER_CHUNK] |
+// hist[P] | cursor[P], hist zero on entry).  guard: the workspace is the index's, shared by
+// calls on any stream, so a launch waits for the previous one to have read it.
+hipError_t launch_ordered(bs_index ix, Plan pl, uint64_t nq, hipStream_t s, uint32_t* ows, bool guard) {
     const bsd::SearchParams all = pl.p;
     const uint32_t g = pl.g, X = ix->xcds;
-    hipError_t e = hipStreamWaitEvent(s, ix->ws_free, 0);  // an earlier launch may still read the map
+    hipError_t e = guard ? hipStreamWaitEvent(s, ix->ws_free, 0) : hipSuccess;
     for (uint64_t c0 = 0; e == hipSuccess && c0 < nq; c0 += ORDER_CHUNK) {
         const uint64_t m = std::min(ORDER_CHUNK, nq - c0);
         bso::OrderParams o;
@@ -518,8 +521,8 @@ hipError_t launch_ordered(bs_index ix, Plan pl, uint64_t nq, hipStream_t s) {
         o.dim = all.dim;
         o.pivT = ix->d_pivT;
         o.pnorm = ix->d_pnorm;
-        o.key = ix->d_ows;
-        o.qmap = ix->d_ows + ORDER_CHUNK;
+        o.key = ows;
+        o.qmap = ows + ORDER_CHUNK;
         o.hist = o.qmap + ORDER_CHUNK;
         o.cursor = o.hist + bso::ORDER_P;
         o.g = g;
@@ -544,7 +547,7 @@ hipError_t launch_ordered(bs_index ix, Plan pl, uint64_t nq, hipStream_t s) {
         pl.grid = dim3(static_cast<uint32_t>(B));
         e = launch(pl, s);
     }
-    if (e == hipSuccess) e = hipEventRecord(ix->ws_free, s);
+    if (e == hipSuccess && guard) e = hipEventRecord(ix->ws_free, s);
     return e;
 }
 
@@ -573,7 +576,7 @@ extern "C" int bs_search_device(bs_index ix, const bs_search_cfg* cfg, const flo
         HIP_TRY(hipEventRecord(e0, s));
     }
     const bool order = ix->order_mode == 2 || (ix->order_mode == 1 && nq >= ORDER_MIN_NQ);
-    hipError_t le = order ? launch_ordered(ix, pl, nq, s) : launch(pl, s);
+    hipError_t le = order ? launch_ordered(ix, pl, nq, s, ix->d_ows, true) : launch(pl, s);
     if (le != hipSuccess) {
         if (e0) (void)hipEventDestroy(e0);
         if (e1) (void)hipEventDestroy(e1);
@@ -648,6 +651,87 @@ extern "C" int bs_search(bs_index ix, const bs_search_cfg* cfg, const float* que
     }
     if (rc == BS_OK && stats) *stats = st;
     return rc;
+} catch (...) {
+    return bs_internal_exception();
+}
+
+// ---------------------------------------------------------------------------------------
+// bs_search_device_noalloc: bs_search_device whose query-scheduling workspace is a static
+// device array instead of the index's, so that a call allocates nothing (for callers that
+// cannot allocate: code under HIP graph capture, serving loops, harnesses that forbid it).
+// ---------------------------------------------------------------------------------------
+// key[ORDER_CHUNK] | qmap[ORDER_CHUNK] | hist[ORDER_P] | cursor[ORDER_P]: 2 MiB + 2 KiB,
+// one copy per GPU for the life of the process.  Host code never uses this name as an
+// address: the device address comes from hipGetSymbolAddress (noalloc_workspace).
+constexpr size_t NOALLOC_WORDS = 2 * ORDER_CHUNK + 2 * bso::ORDER_P;
+static __device__ __align__(256) uint32_t scratch[NOALLOC_WORDS];
+
+namespace {
+
+constexpr int MAX_DEVICES = 64;
+std::mutex g_scratch_mutex;
+uint32_t* g_scratch_ptr[MAX_DEVICES] = {};
+
+// this device's address of `scratch`, looked up once per device with that device current
+int noalloc_workspace(int dev, uint32_t** out) {
+    if (dev < 0 || dev >= MAX_DEVICES) return fail(BS_EINVAL, "device ordinal out of range");
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    if (!g_scratch_ptr[dev]) {
+        void* ptr = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !ptr)
+            return fail(BS_EHIP, std::string("hipGetSymbolAddress(scratch) failed: ") + hipGetErrorString(e));
+        g_scratch_ptr[dev] = static_cast<uint32_t*>(ptr);
+    }
+    *out = g_scratch_ptr[dev];
+    return BS_OK;
+}
+
+// fill kernel for the histogram (no memset node, so the call can be captured in a graph)
+__global__ void __launch_bounds__(256) clear_words(uint32_t* w, uint32_t n) {
+    const uint32_t i = blockIdx.x * 256 + threadIdx.x;
+    if (i < n) w[i] = 0u;
+}
+
+}  // namespace
+
+extern "C" int bs_search_device_noalloc(bs_index ix, const bs_search_cfg* cfg, const float* d_queries, uint64_t nq,
+                                        uint32_t* d_results, float* d_dists, uint32_t* d_per_query,
+                                        void* stream) try {
+    if (nq > ORDER_CHUNK)
+        return fail(BS_EINVAL, "bs_search_device_noalloc: nq = " + std::to_string(nq) + " exceeds the " +
+                                   std::to_string(ORDER_CHUNK) + " queries its static workspace holds; split the batch");
+    Plan pl;
+    int rc = make_plan(ix, cfg, nq, pl);
+    if (rc) return rc;
+    if (nq == 0) return BS_OK;
+    if (!d_queries || !d_results) return fail(BS_EINVAL, "queries and results must be given");
+    int dev = 0;
+    HIP_TRY(hipGetDevice(&dev));
+    if (dev != ix->device)
+        return fail(BS_EINVAL, "the index lives on device " + std::to_string(ix->device) + ", the current device is " +
+                                   std::to_string(dev));
+    pl.p.queries = d_queries;
+    pl.p.results = d_results;
+    pl.p.dists = d_dists;
+    pl.p.per_query = d_per_query;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const bool order = ix->order_mode == 2 || (ix->order_mode == 1 && nq >= ORDER_MIN_NQ);
+    hipError_t le = hipSuccess;
+    if (order) {
+        uint32_t* ws = nullptr;
+        rc = noalloc_workspace(dev, &ws);
+        if (rc) return rc;
+        // the histogram must start at zero; the previous call's contents stay otherwise
+        hipLaunchKernelGGL(clear_words, dim3((bso::ORDER_P + 255) / 256), dim3(256), 0, s, ws + 2 * ORDER_CHUNK,
+                           bso::ORDER_P);
+        le = hipGetLastError();
+        if (le == hipSuccess) le = launch_ordered(ix, pl, nq, s, ws, false);
+    } else {
+        le = launch(pl, s);
+    }
+    if (le != hipSuccess) return fail(BS_EHIP, std::string("search launch failed: ") + hipGetErrorString(le));
+    return BS_OK;
 } catch (...) {
     return bs_internal_exception();
 }

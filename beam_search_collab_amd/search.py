@@ -186,6 +186,19 @@ class GPUGraph:
         return st.as_dict()
 
 
+    def search_device_noalloc(self, d_queries: int, nq: int, d_results: int, K: int, mode: str, cfg,
+                              d_dists: int = 0, d_per_query: int = 0, stream: int = 0):
+        """bs_search_device_noalloc: the same search, asynchronous on `stream`, allocating
+        nothing (its scheduling workspace is a static device array; at most 262144 queries)."""
+        m, ny = MODES[mode]
+        c = make_cfg(m, ny, K, cfg)
+        _check(_lib.hip().bs_search_device_noalloc(self._h, C.byref(c), C.c_void_p(d_queries), nq,
+                                                   C.c_void_p(d_results), C.c_void_p(d_dists) if d_dists else None,
+                                                   C.c_void_p(d_per_query) if d_per_query else None,
+                                                   C.c_void_p(stream) if stream else None),
+               "bs_search_device_noalloc")
+
+
 def build_vamana_device(vecs: np.ndarray, degree: int = 32, beam_width: int = 128, alpha: float = 2.0,
                         seed: int = 1234, verbose: bool = False) -> np.ndarray:
     """build_graph (src/build_graph.cpp) on the device: the reference's graph, edge for

@@ -106,6 +106,19 @@ int bs_search_device(bs_index idx, const bs_search_cfg* cfg, const float* d_quer
                      uint64_t nq, uint32_t* d_results, float* d_dists, uint32_t* d_per_query,
                      void* stream, int sync, bs_stats* stats);
 
+/* bs_search_device without allocation.  No counterpart in the reference: for callers
+ * that cannot allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  The query-scheduling workspace (labels, launch map,
+ * bucket counters) is a static device array of 2 MiB + 2 KiB per GPU, held until the process
+ * ends, instead of the index's; the call allocates nothing and records no event.  At most
+ * 262144 queries per call (the workspace's size; larger nq is rejected with BS_EINVAL).
+ * Asynchronous on `stream`; buffers as for bs_search_device.  Every call on one GPU shares
+ * the array: calls that overlap on one GPU (other streams, other threads) race; calls in
+ * order on one stream do not.  The current device must be the index's. */
+int bs_search_device_noalloc(bs_index idx, const bs_search_cfg* cfg, const float* d_queries,
+                             uint64_t nq, uint32_t* d_results, float* d_dists,
+                             uint32_t* d_per_query, void* stream);
+
 /* Query scheduling (no counterpart in the reference, whose launches run query i in
  * block i, src/gpu_cli.cu:94-95,111-112,128-129).  Queries are independent, so their order
  * changes no result; it changes where their gathers hit.  With scheduling on, a search
