@@ -413,12 +413,12 @@ int make_plan(bs_index ix, const bs_search_cfg* cfg, uint64_t nq, Plan& pl) {
     p.reset = cfg->reset_interval;
     p.L = L;
     // The hash filters (visit filter, RaBitQ expanded set) refuse keys as the reference's
-    // table of 2^ceil(log2 capacity) slots does, but get twice as many slots (up to 2048)
-    // when the workgroup's LDS allows it: probe runs at the same occupancy are shorter, the
-    // results are the same.  The visit filter fills up between resets (config B: 5.0 -> 4.8
-    // ms, topk 512: 20.1 -> 10.9 ms); the RaBitQ expanded set holds about 1.2 T keys, so it
-    // is doubled only past T = 0.4 x slots (topk 768: 22.4 -> 14.7 ms), since at topk 256
-    // the larger table costs more wavefronts per CU than it saves (3.35 -> 3.5 ms).
+    // table of 2^ceil(log2 capacity) slots does, but get more slots when the workgroup's LDS
+    // allows it: probe runs at the same occupancy are shorter, the results are the same.
+    // The visit filter fills up between resets and gets twice the slots (config B: 5.0 ->
+    // 4.8 ms, topk 512: 20.1 -> 10.9 ms).  The RaBitQ expanded set ends with about one key
+    // per beam slot and gets 5T/3 slots within [cap, 2 cap] (topk 768: 2048 slots 14.0 ms,
+    // 1280 slots 12.8 ms: fewer slots, more wavefronts per CU).
     uint32_t scratch = 512u * pl.TR;
     if (mode == BS_RABITQ) {
         p.pdim = ix->pdim;
@@ -453,12 +453,20 @@ int make_plan(bs_index ix, const bs_search_cfg* cfg, uint64_t nq, Plan& pl) {
     } else {
         const uint32_t b = log2_ceil(cap);
         p.filter_cap = 1u << b;
-        const bool grow = b < 11 && (mode != BS_RABITQ || 5ull * T > 2ull * p.filter_cap);
-        p.filter_bits = grow ? b + 1 : b;
-        layout((1u << p.filter_bits) * 4);
-        if (static_cast<size_t>(p.lds_wave) * ny > ix->max_lds && p.filter_bits > b) {
-            p.filter_bits = b;
-            layout((1u << b) * 4);
+        const uint32_t base_slots = std::max(4u, p.filter_cap);
+        if (mode != BS_RABITQ) {
+            // the visit filter fills up to cap between resets: twice the slots (a power of two)
+            p.filter_slots = b < 11 ? base_slots * 2u : base_slots;
+        } else {
+            // the expanded set holds about one key per beam slot: 5T/3 slots (a multiple of
+            // 64), at least cap and at most 2 cap
+            const uint64_t want = (5ull * T / 3 + 63) / 64 * 64;
+            p.filter_slots = static_cast<uint32_t>(std::min<uint64_t>(2ull * base_slots, std::max<uint64_t>(base_slots, want)));
+        }
+        layout(p.filter_slots * 4u);
+        if (static_cast<size_t>(p.lds_wave) * ny > ix->max_lds && p.filter_slots > base_slots) {
+            p.filter_slots = base_slots;
+            layout(p.filter_slots * 4u);
         }
     }
     // base mode with too few queries to give every SIMD 4 wavefronts: 2 or 4 wavefronts

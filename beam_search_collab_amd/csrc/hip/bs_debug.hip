@@ -334,12 +334,10 @@ __global__ void __launch_bounds__(64) dbg_filter_kernel(int bloom, uint32_t bits
     extern __shared__ __attribute__((aligned(16))) char smem[];
     const uint32_t lane = bsd::lane_id();
     if (!bloom) {
-        bsd::HashLds h;
+        bsd::HashLds<true> h;
         h.t = reinterpret_cast<uint32_t*>(smem);
-        h.bits = bits;
-        h.size = 1u << bits;
-        h.mask = h.size - 1;
-        h.cap = h.size;
+        h.size = (1u << bits) >= 4u ? (1u << bits) : 4u;
+        h.cap = 1u << bits;
         h.clear();
         for (uint32_t b = 0; b < nbatch; ++b) {
             const uint32_t k = lane < bsize ? keys[static_cast<uint64_t>(b) * bsize + lane] : bsd::INVALID;
@@ -374,7 +372,7 @@ extern "C" int bs_debug_filter(int bloom, uint32_t capacity, const uint32_t* key
         if (bits < 5) bits = 5;
         lds = (size_t(1) << (bits - 5)) * 4;
     } else {
-        lds = (size_t(1) << bits) * 4;
+        lds = std::max<size_t>(16, (size_t(1) << bits) * 4);
     }
     if (lds > 65536) return dfail(BS_EINVAL, "capacity too large for the primitive test");
     DevBuf<uint32_t> dk, dn, dq, dc;

@@ -323,19 +323,39 @@ __device__ __forceinline__ void sort_beam(uint64_t (&v)[TR]) {
 // visit filters in the wave's LDS slice
 // ---------------------------------------------------------------------------
 
-// HashFilter (filter_hash.cuh:11-99): 2^bits slots, h = (k ^ (k >> bits)) & mask, linear
-// probing, empty = 0xFFFFFFFF.  `occ` counts occupied slots (wave-uniform).
-// The reference's table (filter_hash.cuh) has cap = 2^ceil(log2 capacity) slots and refuses
-// keys once full; membership itself does not depend on where keys sit, so this table may
-// have more slots (size >= cap) for shorter probe runs and still refuse exactly the keys
-// the reference refuses: the occupancy is checked against cap.
+// HashFilter (filter_hash.cuh:11-99): an LDS set of node ids with linear probing, empty =
+// 0xFFFFFFFF, that refuses keys once `cap` are stored (the reference's table has cap =
+// 2^ceil(log2 capacity) slots).  Membership does not depend on where keys sit, so the table
+// may have more slots than cap (shorter probe runs).  A key's probe sequence is the slots
+// from its home slot on; it sits in the first empty slot of its sequence at insertion and
+// slots never empty, so a lookup stops at the key (present) or an empty slot (absent).
+// Inserts go slot by slot (a compare-and-swap returns the slot's key); lookups read 4 slots
+// (16 B, one ds_read_b128) per step.  `occ` counts occupied slots (wave-uniform).
+//   POW2: 2^k slots, home = (k ^ (k >> log2 size)) & (size - 1) (the reference's hash);
+//   else: any multiple of 4 slots, home = (k * 0x9e3779b1) scaled to [0, size).
+template <bool POW2>
 struct HashLds {
     uint32_t* t;
-    uint32_t bits, size, mask;
-    uint32_t cap;
+    uint32_t size;  // slots, a multiple of 4 (a power of two when POW2)
+    uint32_t cap;   // keys accepted
     uint32_t occ;
 
-    __device__ __forceinline__ uint32_t slot0(uint32_t k) const { return (k ^ (k >> bits)) & mask; }
+    __device__ __forceinline__ uint32_t home(uint32_t k) const {
+        if constexpr (POW2) {
+            const uint32_t b = static_cast<uint32_t>(__builtin_ctz(size));
+            return (k ^ (k >> b)) & (size - 1u);
+        } else {
+            return static_cast<uint32_t>((static_cast<uint64_t>(k * 0x9E3779B1u) * size) >> 32);
+        }
+    }
+    __device__ __forceinline__ uint32_t next(uint32_t i) const {
+        if constexpr (POW2) return (i + 1) & (size - 1u);
+        else return i + 1 == size ? 0u : i + 1;
+    }
+    __device__ __forceinline__ uint32_t add(uint32_t i, uint32_t d) const {  // d < size
+        if constexpr (POW2) return (i + d) & (size - 1u);
+        else return i + d >= size ? i + d - size : i + d;
+    }
 
     __device__ __forceinline__ void clear() {
         const uint32_t lane = lane_id();
@@ -350,10 +370,10 @@ struct HashLds {
     __device__ __forceinline__ uint32_t insert1(uint32_t k) {
         if (occ >= cap) return 0u;  // full: present or rejected, 0 either way
         const uint32_t lane = lane_id();
-        const uint32_t h = slot0(k);
+        const uint32_t h = home(k);
         for (uint32_t base = 0; base < size; base += 64) {
             const uint32_t off = base + lane;
-            const uint32_t idx = (h + off) & mask;
+            const uint32_t idx = add(h, off < size ? off : 0u);
             const uint32_t s = (off < size) ? t[idx] : 0u;
             const uint64_t hit = ballot(off < size && s == k);
             const uint64_t emp = ballot(off < size && s == INVALID);
@@ -371,20 +391,31 @@ struct HashLds {
     }
 
     __device__ __forceinline__ bool contains_lane(uint32_t k) const {
-        uint32_t idx = slot0(k);
-        for (uint32_t i = 0; i < size; ++i) {
-            const uint32_t s = t[idx];
-            if (s == k) return true;
-            if (s == INVALID) return false;
-            idx = (idx + 1) & mask;
+        const uint32_t s0 = home(k);
+        const uint32_t nq = size >> 2;
+        uint32_t q = s0 >> 2;
+        // the slots before the home slot in its group of 4 are not in k's sequence (they
+        // end it, after a full turn)
+        const uint32_t f = s0 & 3u;
+        uint4 v = reinterpret_cast<const uint4*>(t)[q];
+        bool hit = (v.x == k && f == 0) || (v.y == k && f <= 1) || (v.z == k && f <= 2) || v.w == k;
+        bool emp = (v.x == INVALID && f == 0) || (v.y == INVALID && f <= 1) || (v.z == INVALID && f <= 2) ||
+                   v.w == INVALID;
+        for (uint32_t i = 0; i < nq; ++i) {
+            if (hit) return true;
+            if (emp) return false;
+            q = q + 1 == nq ? 0u : q + 1;
+            v = reinterpret_cast<const uint4*>(t)[q];
+            hit = v.x == k || v.y == k || v.z == k || v.w == k;
+            emp = v.x == INVALID || v.y == INVALID || v.z == INVALID || v.w == INVALID;
         }
-        return false;
+        return hit;
     }
 
     // lane-parallel batch (one key per lane, INVALID = idle).  Sequential semantics in
     // lane order (DESC: from lane 63 down): when the batch cannot fill the table, every
-    // lane inserts concurrently with LDS compare-and-swap (membership does not depend on
-    // the order); otherwise the keys are inserted one by one in that order.  Returns 1 for
+    // lane inserts concurrently with LDS compare-and-swap (membership does not depend on the
+    // order); otherwise the keys are inserted one by one in that order.  Returns 1 for
     // newly inserted keys.
     template <bool DESC = false>
     __device__ __forceinline__ uint32_t insert_batch(uint32_t k) {
@@ -397,7 +428,7 @@ struct HashLds {
         // batch changes nothing (filter_hash.cuh:78-86 probes all slots to the same end).
         if (nv == 0 || occ >= cap) return 0;
         if (occ + nv <= cap) {
-            uint32_t idx = slot0(k);
+            uint32_t idx = home(k);
             bool done = !valid;
             for (uint32_t step = 0; step <= size; ++step) {
                 if (ballot(!done) == 0) break;
@@ -409,7 +440,7 @@ struct HashLds {
                     } else if (old == k) {
                         done = true;
                     } else {
-                        idx = (idx + 1) & mask;
+                        idx = next(idx);
                     }
                 }
             }

@@ -26,8 +26,9 @@ struct SearchParams {
     const uint32_t* qmap;   // nq: launch position -> query, or null (identity)
     uint64_t nq;
     uint32_t dim, dstride, R, K, T;
-    uint32_t filter_bits;   // hash: log2 slots; bloom: log2 bits
-    uint32_t filter_cap;    // hash: keys the table accepts (the reference's slot count)
+    uint32_t filter_bits;     // bloom: log2 bits
+    uint32_t filter_slots;    // hash: slots (a multiple of 4)
+    uint32_t filter_cap;      // hash: keys the table accepts (the reference's slot count)
     uint32_t entry;
     int32_t max_it, reset;
     uint32_t pdim, wpp, rec_words, rec_ids, rec_fac, rec_codes;  // record offsets (words)
@@ -96,13 +97,11 @@ search_kernel(const SearchParams p) {
             return;
         }
 
-        HashLds hf;
+        HashLds<true> hf;
         BloomLds bf;
         if constexpr (MODE == MODE_HASH) {
             hf.t = reinterpret_cast<uint32_t*>(my + p.off_filter);
-            hf.bits = p.filter_bits;
-            hf.size = 1u << p.filter_bits;
-            hf.mask = hf.size - 1;
+            hf.size = p.filter_slots;
             hf.cap = p.filter_cap;
             hf.clear();
         } else {
@@ -238,11 +237,9 @@ search_kernel(const SearchParams p) {
         }
     } else {
         // ---------------------------------------------------------------- rabitq
-        HashLds hf;
+        HashLds<false> hf;
         hf.t = reinterpret_cast<uint32_t*>(my + p.off_filter);
-        hf.bits = p.filter_bits;
-        hf.size = 1u << p.filter_bits;
-        hf.mask = hf.size - 1;
+        hf.size = p.filter_slots;
         hf.cap = p.filter_cap;
         const uint32_t wpp = p.wpp;
         const uint64_t rstride = p.rec_words;
