@@ -419,7 +419,7 @@ int make_plan(bs_index ix, const bs_search_cfg* cfg, uint64_t nq, Plan& pl) {
     // 4.8 ms, topk 512: 20.1 -> 10.9 ms).  The RaBitQ expanded set ends with about one key
     // per beam slot and gets 5T/3 slots within [cap, 2 cap] (topk 768: 2048 slots 14.0 ms,
     // 1280 slots 12.8 ms: fewer slots, more wavefronts per CU).
-    uint32_t scratch = 512u * pl.TR;
+    uint32_t scratch = 512u * pl.TR + 16u;  // the beam and the merge's dump slot
     if (mode == BS_RABITQ) {
         p.pdim = ix->pdim;
         p.wpp = ix->wpp;

@@ -226,7 +226,7 @@ __global__ void __launch_bounds__(64) dbg_beam_kernel(uint32_t T, const uint64_t
             ck[rc] = (j < bsize) ? keys[static_cast<uint64_t>(b) * bsize + j] : bsd::EMPTY_KEY;
             cm[rc] = bsd::ballot(ck[rc] != bsd::EMPTY_KEY);
         }
-        bsd::beam_merge<TR, CR>(beam, ck, cm, T, scratch, scratch + 64 * TR);
+        bsd::beam_merge<TR, CR>(beam, ck, cm, T, scratch, scratch + 64 * TR + 2);
         for (uint32_t k = 0; k < picks; ++k) {
             const uint32_t id = bsd::beam_pick<TR, RUN>(beam);
             if (lane == 0) picked[static_cast<uint64_t>(b) * picks + k] = id;
@@ -242,7 +242,7 @@ __global__ void __launch_bounds__(64) dbg_beam_kernel(uint32_t T, const uint64_t
 template <int TR, int CR>
 static void launch_beam(int run, uint32_t T, const uint64_t* k, uint32_t nb, uint32_t bs, uint32_t picks,
                         uint32_t* pk, uint64_t* bo) {
-    const size_t lds = 512u * TR + 8u * (64u + (TR > 8 ? TR : 8));  // merge scratch + aux
+    const size_t lds = 512u * TR + 16u + 8u * (64u + (TR > 8 ? TR : 8));  // merge scratch (+ dump slot) + aux
     if (run)
         hipLaunchKernelGGL((dbg_beam_kernel<TR, CR, true>), dim3(1), dim3(64), lds, nullptr, T, k, nb, bs, picks, pk, bo);
     else

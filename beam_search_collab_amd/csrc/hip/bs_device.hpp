@@ -64,7 +64,7 @@ __device__ __forceinline__ uint32_t key_id(uint64_t k) { return static_cast<uint
 // Identical keys are indistinguishable, so the two orders of equal candidates agree.
 // Both loops use the sorted merge for one candidate register (degree <= 64); the kernels
 // that would lose a wavefront per SIMD to its registers are compiled for 5 waves per SIMD.
-// LDS: scratch = 64*TR keys, aux = 64 + TR keys.
+// LDS: scratch = 64*TR + 1 keys (the last one a dump slot), aux = 64 + TR keys.
 // ---------------------------------------------------------------------------
 // The rank loop costs ~(9 + 2 TR) instructions per candidate, the sorted merge a roughly
 // fixed ~250 plus LDS latency: the crossover falls with the beam size.
@@ -113,10 +113,12 @@ __device__ __forceinline__ void beam_merge_sorted(uint64_t (&beam)[TR], uint64_t
     for (uint32_t step = 32; step >= 1; step >>= 1)
         if (B[lo + step - 1] <= c) lo += step;
     const uint32_t pos = lane + lo;
-    if (lane < n) {
-        C[lane] = c;
-        if (pos < T) __hip_atomic_fetch_or(&M[pos >> 6], 1ull << (pos & 63u), __ATOMIC_RELAXED,
-                                           __HIP_MEMORY_SCOPE_WAVEFRONT);
+    C[lane] = c;  // sorted (EMPTY past n)
+    {
+        // every lane ors a word (0 unless it places a candidate): no divergent branch
+        const bool place = lane < n && pos < T;
+        __hip_atomic_fetch_or(&M[place ? (pos >> 6) : 0u], place ? 1ull << (pos & 63u) : 0ull, __ATOMIC_RELAXED,
+                              __HIP_MEMORY_SCOPE_WAVEFRONT);
     }
     wave_sync();
     uint32_t before = 0;  // candidates in the slots of earlier registers
@@ -126,7 +128,10 @@ __device__ __forceinline__ void beam_merge_sorted(uint64_t (&beam)[TR], uint64_t
         const uint32_t s = static_cast<uint32_t>(r) * 64u + lane;
         const uint32_t ob = before + bsw::lanes_below(mw);
         const bool occ = (mw >> lane) & 1ull;
-        const uint64_t v = occ ? C[ob] : B[s - ob];
+        // both reads unconditional (a conditional LDS read becomes an exec-mask branch)
+        const uint64_t vc = C[ob < 64u ? ob : 63u];
+        const uint64_t vb = B[s - ob];
+        const uint64_t v = occ ? vc : vb;
         beam[r] = (s < T) ? v : EMPTY_KEY;
         before += static_cast<uint32_t>(__builtin_popcountll(mw));
     }
@@ -188,17 +193,22 @@ __device__ __forceinline__ void beam_merge(uint64_t (&beam)[TR], const uint64_t 
             }
         }
     }
+    // unconditional scatter and gather (a conditional LDS access becomes an exec-mask
+    // branch): keys landing at T or beyond go to the dump slot 64*TR
+    constexpr uint32_t DUMP = 64u * TR;
 #pragma unroll
-    for (int r = 0; r < TR; ++r)
-        if (bpos[r] < T) lds_scratch[bpos[r]] = beam[r];
+    for (int r = 0; r < TR; ++r) lds_scratch[bpos[r] < T ? bpos[r] : DUMP] = beam[r];
 #pragma unroll
-    for (int rc = 0; rc < CR; ++rc)
-        if (((cmask[rc] >> lane) & 1ull) && cpos[rc] < T) lds_scratch[cpos[rc]] = ck[rc];
+    for (int rc = 0; rc < CR; ++rc) {
+        const bool w = ((cmask[rc] >> lane) & 1ull) && cpos[rc] < T;
+        lds_scratch[w ? cpos[rc] : DUMP] = ck[rc];
+    }
     wave_sync();
 #pragma unroll
     for (int r = 0; r < TR; ++r) {
         const uint32_t e = static_cast<uint32_t>(r) * 64u + lane;
-        beam[r] = (e < T) ? lds_scratch[e] : EMPTY_KEY;
+        const uint64_t v = lds_scratch[e];
+        beam[r] = (e < T) ? v : EMPTY_KEY;
     }
     wave_sync();
 }
@@ -208,35 +218,40 @@ __device__ __forceinline__ void beam_merge(uint64_t (&beam)[TR], const uint64_t 
 // id (INVALID if none).  RUN = true (the rabitq beam may hold identical keys): of a run
 // of identical keys the last one is marked, which keeps the beam sorted.
 // ---------------------------------------------------------------------------
+// register r (wave-uniform r) of the beam, by a tree of selects on the bits of r
+template <int TR>
+__device__ __forceinline__ uint64_t beam_reg(const uint64_t (&beam)[TR], uint32_t r) {
+    uint64_t v[TR];
+#pragma unroll
+    for (int i = 0; i < TR; ++i) v[i] = beam[i];
+#pragma unroll
+    for (int step = 1; step < TR; step <<= 1) {
+#pragma unroll
+        for (int i = 0; i + step < TR; i += 2 * step) v[i] = (r & static_cast<uint32_t>(step)) ? v[i + step] : v[i];
+    }
+    return v[0];
+}
+
 template <int TR, bool RUN>
 __device__ __forceinline__ uint32_t beam_pick(uint64_t (&beam)[TR]) {
     const uint32_t lane = lane_id();
-    // first register holding an unexpanded key, and that key's lane: scalar selects over
-    // the registers' ballots (no branches)
-    uint32_t pr = TR;
-    uint64_t mp = 0;
+    // registers holding an unexpanded key; the first one, its first such lane
+    uint32_t nz = 0;
 #pragma unroll
-    for (int r = TR - 1; r >= 0; --r) {
-        const uint64_t m = ballot((static_cast<uint32_t>(beam[r]) & 1u) == 0u);
-        pr = m != 0 ? static_cast<uint32_t>(r) : pr;
-        mp = m != 0 ? m : mp;
-    }
-    if (pr == static_cast<uint32_t>(TR)) return INVALID;
+    for (int r = 0; r < TR; ++r)
+        nz |= (ballot((static_cast<uint32_t>(beam[r]) & 1u) == 0u) != 0) ? (1u << r) : 0u;
+    if (nz == 0) return INVALID;
+    const uint32_t pr = static_cast<uint32_t>(__builtin_ctz(nz));
+    const uint64_t row = beam_reg<TR>(beam, pr);
+    const uint64_t mp = ballot((static_cast<uint32_t>(row) & 1u) == 0u);
     const uint32_t pl = static_cast<uint32_t>(__builtin_ctzll(mp));
-    // the register is chosen by vector selects under a uniform condition, then one
-    // readlane (a readlane per register under a branch costs a branch per register)
-    uint64_t row = beam[0];
-#pragma unroll
-    for (int r = 1; r < TR; ++r) row = (pr == static_cast<uint32_t>(r)) ? beam[r] : row;
     const uint64_t kp = readlane64(row, pl);
     uint32_t qr = pr, ql = pl;
     if constexpr (RUN) {
         // identical keys are rare: look at the next element first, scan only if it repeats
-        const uint32_t nr = pl < 63u ? pr : pr + 1u;
-        uint64_t rown = EMPTY_KEY;
-#pragma unroll
-        for (int r = 0; r < TR; ++r) rown = (nr == static_cast<uint32_t>(r)) ? beam[r] : rown;
-        const uint64_t nxt = readlane64(rown, (pl + 1u) & 63u);
+        uint64_t nxt = EMPTY_KEY;
+        if (pl < 63u) nxt = readlane64(row, pl + 1u);
+        else if (pr + 1u < static_cast<uint32_t>(TR)) nxt = readlane64(beam_reg<TR>(beam, pr + 1u), 0u);
         if (nxt == kp) {
 #pragma unroll
             for (int r = 0; r < TR; ++r) {

@@ -41,11 +41,18 @@ struct SearchParams {
     L2Shape L;
 };
 
-// Beams up to 256 with one candidate register and rows of at most 128 dims (PB = 2; the
-// RaBitQ loop always) are compiled for 5 wavefronts per SIMD (at most 96 VGPRs): the sorted
-// merge would otherwise take them to 4.
+// Register budget per instance, matched to what the LDS slice allows anyway: RaBitQ beams
+// up to 256 (about 7 KB of LDS per wavefront) are compiled for 5 wavefronts per SIMD (at most
+// 96 VGPRs); the base loop with beams up to 256 and rows of at most 128 dims (PB = 2) holds
+// a 2048-slot filter (about 11 KB, at most 15 wavefronts per CU), so it gets 4 (128 VGPRs,
+// no spills).
+template <int TR, int CR, int MODE, int PB>
+constexpr int min_waves_per_simd() {
+    return (CR != 1 || TR > 4) ? 1 : MODE == MODE_RABITQ ? 5 : PB == 2 ? 4 : 1;
+}
+
 template <int TR, int CR, int QMAX, int MODE, int PB>
-__global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu((MODE == MODE_RABITQ || PB == 2) && TR <= 4 && CR == 1 ? 5 : 1, 8)))
+__global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(min_waves_per_simd<TR, CR, MODE, PB>(), 8)))
 search_kernel(const SearchParams p) {
     extern __shared__ __attribute__((aligned(16))) char smem[];
     const uint32_t lane = lane_id();
