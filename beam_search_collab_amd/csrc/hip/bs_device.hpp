@@ -143,11 +143,7 @@ __device__ __forceinline__ void beam_merge(uint64_t (&beam)[TR], const uint64_t 
                                            const uint64_t (&cmask_in)[CR], uint32_t T,
                                            uint64_t* lds_scratch, uint64_t* lds_aux) {
     const uint32_t lane = lane_id();
-    uint64_t thr = EMPTY_KEY;
-    const uint32_t lr = (T - 1) >> 6, ll = (T - 1) & 63u;
-#pragma unroll
-    for (int r = 0; r < TR; ++r)
-        if (static_cast<uint32_t>(r) == lr) thr = readlane64(beam[r], ll);
+    const uint64_t thr = readlane64(beam[(T - 1) >> 6], (T - 1) & 63u);
     uint64_t cmask[CR];
     uint32_t n = 0;
 #pragma unroll
@@ -218,18 +214,10 @@ __device__ __forceinline__ void beam_merge(uint64_t (&beam)[TR], const uint64_t 
 // id (INVALID if none).  RUN = true (the rabitq beam may hold identical keys): of a run
 // of identical keys the last one is marked, which keeps the beam sorted.
 // ---------------------------------------------------------------------------
-// register r (wave-uniform r) of the beam, by a tree of selects on the bits of r
+// register r of the beam (wave-uniform r: a register-indexed move, s_set_gpr_idx)
 template <int TR>
 __device__ __forceinline__ uint64_t beam_reg(const uint64_t (&beam)[TR], uint32_t r) {
-    uint64_t v[TR];
-#pragma unroll
-    for (int i = 0; i < TR; ++i) v[i] = beam[i];
-#pragma unroll
-    for (int step = 1; step < TR; step <<= 1) {
-#pragma unroll
-        for (int i = 0; i + step < TR; i += 2 * step) v[i] = (r & static_cast<uint32_t>(step)) ? v[i + step] : v[i];
-    }
-    return v[0];
+    return beam[r];
 }
 
 template <int TR, bool RUN>
@@ -263,13 +251,8 @@ __device__ __forceinline__ uint32_t beam_pick(uint64_t (&beam)[TR]) {
             }
         }
     }
-    // set the mark (key LSB) of element (qr, ql): only the low word changes
-    const uint32_t bit = (lane == ql) ? 1u : 0u;
-#pragma unroll
-    for (int r = 0; r < TR; ++r) {
-        const uint32_t lo = static_cast<uint32_t>(beam[r]) | ((qr == static_cast<uint32_t>(r)) ? bit : 0u);
-        beam[r] = (beam[r] & 0xFFFFFFFF00000000ull) | lo;
-    }
+    // set the mark (key LSB) of element (qr, ql)
+    beam[qr] |= (lane == ql) ? 1ull : 0ull;
     return key_id(kp);
 }
 
