@@ -73,18 +73,43 @@ __device__ __forceinline__ constexpr uint32_t merge_sort_min() {
     return TR >= 16 ? 3u : TR >= 8 ? 5u : 8u;
 }
 
-// ascending bitonic sort of the first P = pow2ceil(n) lanes (lanes beyond hold EMPTY)
+// EMPTY in the slots at T and beyond (only when T < 64*TR: the gathers above fill
+// every register, the registers past T first)
+template <int TR>
+__device__ __forceinline__ void beam_clear_tail(uint64_t (&beam)[TR], uint32_t T) {
+    if (T >= 64u * TR) return;
+#pragma unroll
+    for (int r = 0; r < TR; ++r) {
+        const uint32_t b = static_cast<uint32_t>(r) * 64u;
+        const uint64_t live = b >= T ? 0ull : (T - b >= 64u ? ~0ull : (1ull << (T - b)) - 1ull);
+        beam[r] = bsw::lane_in(live) ? beam[r] : EMPTY_KEY;
+    }
+}
+
+// lanes whose index has bit s clear (s a power of two; s = 64: every lane)
+__host__ __device__ constexpr uint64_t lanes_bit_clear(uint32_t s) {
+    return s == 1    ? 0x5555555555555555ull
+           : s == 2  ? 0x3333333333333333ull
+           : s == 4  ? 0x0F0F0F0F0F0F0F0Full
+           : s == 8  ? 0x00FF00FF00FF00FFull
+           : s == 16 ? 0x0000FFFF0000FFFFull
+           : s == 32 ? 0x00000000FFFFFFFFull
+                     : ~0ull;
+}
+
+// ascending bitonic sort of the first P = pow2ceil(n) lanes (lanes beyond hold EMPTY).
+// A lane keeps the smaller of its key and its partner's where bit s and bit k of its
+// index agree: a constant lane mask.
 __device__ __forceinline__ uint64_t sort_lanes(uint64_t v, uint32_t n) {
-    const uint32_t lane = lane_id();
 #pragma unroll
     for (uint32_t k = 2; k <= 64; k <<= 1) {
         if (k / 2 >= n) break;
 #pragma unroll
         for (uint32_t s = k >> 1; s >= 1; s >>= 1) {
             const uint64_t p = bsw::xor_lane64_rt(v, s);
-            const bool keep_min = ((lane & s) == 0) == ((lane & k) == 0);
-            const bool lt = p < v;
-            v = (keep_min == lt) ? p : v;
+            const uint64_t keep_min = ~(lanes_bit_clear(s) ^ lanes_bit_clear(k));
+            const uint64_t lt = ballot(p < v);
+            v = bsw::lane_in(~(keep_min ^ lt)) ? p : v;
         }
     }
     return v;
@@ -97,7 +122,7 @@ __device__ __forceinline__ void beam_merge_sorted(uint64_t (&beam)[TR], uint64_t
     uint64_t* C = aux;       // 64 sorted candidates
     uint64_t* M = aux + 64;  // TR words: bit s = output slot s holds a candidate
     // compact the candidates to C[0..n), copy the beam to B, clear the bitmap
-    if ((cmask >> lane) & 1ull) C[bsw::lanes_below(cmask)] = ck;
+    if (bsw::lane_in(cmask)) C[bsw::lanes_below(cmask)] = ck;
 #pragma unroll
     for (int r = 0; r < TR; ++r) B[static_cast<uint32_t>(r) * 64u + lane] = beam[r];
     if (lane < static_cast<uint32_t>(TR)) M[lane] = 0ull;
@@ -127,14 +152,13 @@ __device__ __forceinline__ void beam_merge_sorted(uint64_t (&beam)[TR], uint64_t
         const uint64_t mw = bsw::uniform64(M[r]);
         const uint32_t s = static_cast<uint32_t>(r) * 64u + lane;
         const uint32_t ob = before + bsw::lanes_below(mw);
-        const bool occ = (mw >> lane) & 1ull;
         // both reads unconditional (a conditional LDS read becomes an exec-mask branch)
-        const uint64_t vc = C[ob < 64u ? ob : 63u];
+        const uint64_t vc = C[min(ob, 63u)];
         const uint64_t vb = B[s - ob];
-        const uint64_t v = occ ? vc : vb;
-        beam[r] = (s < T) ? v : EMPTY_KEY;
+        beam[r] = bsw::lane_in(mw) ? vc : vb;
         before += static_cast<uint32_t>(__builtin_popcountll(mw));
     }
+    beam_clear_tail<TR>(beam, T);
     wave_sync();
 }
 
@@ -172,7 +196,6 @@ __device__ __forceinline__ void beam_merge(uint64_t (&beam)[TR], const uint64_t 
             const uint32_t lj = static_cast<uint32_t>(__builtin_ctzll(m));
             m &= m - 1;
             const uint64_t kj = readlane64(ck[rj], lj);
-            const uint32_t jidx = static_cast<uint32_t>(rj) * 64u + lj;
             uint32_t le = 0;
 #pragma unroll
             for (int r = 0; r < TR; ++r) {
@@ -182,30 +205,27 @@ __device__ __forceinline__ void beam_merge(uint64_t (&beam)[TR], const uint64_t 
             }
 #pragma unroll
             for (int rc = 0; rc < CR; ++rc) {
-                const uint32_t idx = static_cast<uint32_t>(rc) * 64u + lane;
-                const bool before = (kj < ck[rc]) || (kj == ck[rc] && jidx < idx);
+                // lanes whose candidate index (rc * 64 + lane) is above candidate j's
+                const uint64_t above = rc < rj ? 0ull : rc > rj ? ~0ull : ~((2ull << lj) - 1ull);
+                const bool before = (kj < ck[rc]) || (kj == ck[rc] && bsw::lane_in(above));
                 cpos[rc] += before ? 1u : 0u;
-                if (rc == rj) cpos[rc] += (lane == lj) ? le : 0u;
+                if (rc == rj) cpos[rc] += bsw::lane_in(1ull << lj) ? le : 0u;
             }
         }
     }
     // unconditional scatter and gather (a conditional LDS access becomes an exec-mask
-    // branch): keys landing at T or beyond go to the dump slot 64*TR
+    // branch).  Positions are a permutation of the beam's 64*TR slots and the candidates;
+    // keys landing at 64*TR or beyond go to the dump slot 64*TR, those landing in
+    // [T, 64*TR) are overwritten with EMPTY after the gather (beam_clear_tail).
     constexpr uint32_t DUMP = 64u * TR;
 #pragma unroll
-    for (int r = 0; r < TR; ++r) lds_scratch[bpos[r] < T ? bpos[r] : DUMP] = beam[r];
+    for (int r = 0; r < TR; ++r) lds_scratch[min(bpos[r], DUMP)] = beam[r];
 #pragma unroll
-    for (int rc = 0; rc < CR; ++rc) {
-        const bool w = ((cmask[rc] >> lane) & 1ull) && cpos[rc] < T;
-        lds_scratch[w ? cpos[rc] : DUMP] = ck[rc];
-    }
+    for (int rc = 0; rc < CR; ++rc) lds_scratch[bsw::lane_in(cmask[rc]) ? min(cpos[rc], DUMP) : DUMP] = ck[rc];
     wave_sync();
 #pragma unroll
-    for (int r = 0; r < TR; ++r) {
-        const uint32_t e = static_cast<uint32_t>(r) * 64u + lane;
-        const uint64_t v = lds_scratch[e];
-        beam[r] = (e < T) ? v : EMPTY_KEY;
-    }
+    for (int r = 0; r < TR; ++r) beam[r] = lds_scratch[static_cast<uint32_t>(r) * 64u + lane];
+    beam_clear_tail<TR>(beam, T);
     wave_sync();
 }
 
@@ -222,7 +242,6 @@ __device__ __forceinline__ uint64_t beam_reg(const uint64_t (&beam)[TR], uint32_
 
 template <int TR, bool RUN>
 __device__ __forceinline__ uint32_t beam_pick(uint64_t (&beam)[TR]) {
-    const uint32_t lane = lane_id();
     // registers holding an unexpanded key; the first one, its first such lane
     uint32_t nz = 0;
 #pragma unroll
@@ -252,7 +271,7 @@ __device__ __forceinline__ uint32_t beam_pick(uint64_t (&beam)[TR]) {
         }
     }
     // set the mark (key LSB) of element (qr, ql)
-    beam[qr] |= (lane == ql) ? 1ull : 0ull;
+    beam[qr] |= bsw::lane_in(1ull << ql) ? 1ull : 0ull;
     return key_id(kp);
 }
 

@@ -18,6 +18,10 @@ __device__ __forceinline__ uint32_t lane_id() {
 
 __device__ __forceinline__ uint64_t ballot(bool p) { return __builtin_amdgcn_ballot_w64(p); }
 
+// this lane's bit of a wave-uniform mask (the mask itself becomes the lane condition: no
+// vector instruction)
+__device__ __forceinline__ bool lane_in(uint64_t m) { return __builtin_amdgcn_inverse_ballot_w64(m); }
+
 // number of set bits of m below this lane
 __device__ __forceinline__ uint32_t lanes_below(uint64_t m) {
     return __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(m >> 32),
