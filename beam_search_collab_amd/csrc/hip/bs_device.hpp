@@ -117,7 +117,7 @@ __device__ __forceinline__ uint64_t sort_lanes(uint64_t v, uint32_t n) {
 
 template <int TR>
 __device__ __forceinline__ void beam_merge_sorted(uint64_t (&beam)[TR], uint64_t ck, uint64_t cmask, uint32_t n,
-                                                  uint32_t T, uint64_t* B, uint64_t* aux) {
+                                                  uint32_t T, uint64_t* B, uint64_t* aux, uint32_t* first) {
     const uint32_t lane = lane_id();
     uint64_t* C = aux;       // 64 sorted candidates
     uint64_t* M = aux + 64;  // TR words: bit s = output slot s holds a candidate
@@ -138,6 +138,7 @@ __device__ __forceinline__ void beam_merge_sorted(uint64_t (&beam)[TR], uint64_t
     for (uint32_t step = 32; step >= 1; step >>= 1)
         if (B[lo + step - 1] <= c) lo += step;
     const uint32_t pos = lane + lo;
+    if (first) *first = min(*first, uniform(pos) >> 6);  // lane 0: the smallest candidate
     C[lane] = c;  // sorted (EMPTY past n)
     {
         // every lane ors a word (0 unless it places a candidate): no divergent branch
@@ -162,10 +163,12 @@ __device__ __forceinline__ void beam_merge_sorted(uint64_t (&beam)[TR], uint64_t
     wave_sync();
 }
 
+// first (optional): the pick's lower bound on the register of the first unexpanded key,
+// lowered to the register where the smallest candidate lands.
 template <int TR, int CR, bool SORTED = true>
 __device__ __forceinline__ void beam_merge(uint64_t (&beam)[TR], const uint64_t (&ck)[CR],
                                            const uint64_t (&cmask_in)[CR], uint32_t T,
-                                           uint64_t* lds_scratch, uint64_t* lds_aux) {
+                                           uint64_t* lds_scratch, uint64_t* lds_aux, uint32_t* first = nullptr) {
     const uint32_t lane = lane_id();
     const uint64_t thr = readlane64(beam[(T - 1) >> 6], (T - 1) & 63u);
     uint64_t cmask[CR];
@@ -178,7 +181,7 @@ __device__ __forceinline__ void beam_merge(uint64_t (&beam)[TR], const uint64_t 
     if (n == 0) return;
     if constexpr (CR == 1 && SORTED) {
         if (n >= merge_sort_min<TR>()) {
-            beam_merge_sorted<TR>(beam, ck[0], cmask[0], n, T, lds_scratch, lds_aux);
+            beam_merge_sorted<TR>(beam, ck[0], cmask[0], n, T, lds_scratch, lds_aux, first);
             return;
         }
     }
@@ -188,6 +191,7 @@ __device__ __forceinline__ void beam_merge(uint64_t (&beam)[TR], const uint64_t 
     uint32_t cpos[CR];
 #pragma unroll
     for (int rc = 0; rc < CR; ++rc) cpos[rc] = 0;
+    uint32_t minle = 64u * TR;  // the smallest candidate's slot: its beam rank
 
 #pragma unroll
     for (int rj = 0; rj < CR; ++rj) {
@@ -203,6 +207,7 @@ __device__ __forceinline__ void beam_merge(uint64_t (&beam)[TR], const uint64_t 
                 bpos[r] += lt ? 1u : 0u;
                 le += static_cast<uint32_t>(__builtin_popcountll(~ballot(lt)));
             }
+            minle = min(minle, le);
 #pragma unroll
             for (int rc = 0; rc < CR; ++rc) {
                 // lanes whose candidate index (rc * 64 + lane) is above candidate j's
@@ -226,6 +231,7 @@ __device__ __forceinline__ void beam_merge(uint64_t (&beam)[TR], const uint64_t 
 #pragma unroll
     for (int r = 0; r < TR; ++r) beam[r] = lds_scratch[static_cast<uint32_t>(r) * 64u + lane];
     beam_clear_tail<TR>(beam, T);
+    if (first) *first = min(*first, minle >> 6);
     wave_sync();
 }
 
@@ -240,17 +246,26 @@ __device__ __forceinline__ uint64_t beam_reg(const uint64_t (&beam)[TR], uint32_
     return beam[r];
 }
 
+// first: a lower bound on the register that holds the first unexpanded key (0 always is
+// one).  Keys only move to later slots, so the bound holds until a merge places a
+// candidate before it (beam_merge lowers it); the pick scans from it and leaves it at the
+// register where it found its key.
 template <int TR, bool RUN>
-__device__ __forceinline__ uint32_t beam_pick(uint64_t (&beam)[TR]) {
-    // registers holding an unexpanded key; the first one, its first such lane
-    uint32_t nz = 0;
-#pragma unroll
-    for (int r = 0; r < TR; ++r)
-        nz |= (ballot((static_cast<uint32_t>(beam[r]) & 1u) == 0u) != 0) ? (1u << r) : 0u;
-    if (nz == 0) return INVALID;
-    const uint32_t pr = static_cast<uint32_t>(__builtin_ctz(nz));
-    const uint64_t row = beam_reg<TR>(beam, pr);
-    const uint64_t mp = ballot((static_cast<uint32_t>(row) & 1u) == 0u);
+__device__ __forceinline__ uint32_t beam_pick(uint64_t (&beam)[TR], uint32_t& first) {
+    // the first register holding an unexpanded key, its first such lane
+    uint32_t pr = first;
+    uint64_t row, mp;
+    for (;;) {
+        if (pr >= static_cast<uint32_t>(TR)) {
+            first = pr;
+            return INVALID;
+        }
+        row = beam_reg<TR>(beam, pr);
+        mp = ballot((static_cast<uint32_t>(row) & 1u) == 0u);
+        if (mp != 0) break;
+        ++pr;
+    }
+    first = pr;
     const uint32_t pl = static_cast<uint32_t>(__builtin_ctzll(mp));
     const uint64_t kp = readlane64(row, pl);
     uint32_t qr = pr, ql = pl;
