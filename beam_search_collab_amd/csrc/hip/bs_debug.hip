@@ -345,7 +345,12 @@ __global__ void __launch_bounds__(64) dbg_filter_kernel(int bloom, uint32_t bits
             const uint32_t r = h.insert_batch(k);
             if (lane < bsize) out_new[static_cast<uint64_t>(b) * bsize + lane] = r;
         }
-        for (uint32_t i = lane; i < nquery; i += 64) out_contains[i] = h.contains_lane(qkeys[i]) ? 1u : 0u;
+        for (uint32_t i0 = 0; i0 < nquery; i0 += 64) {
+            const uint32_t i = i0 + lane;
+            const uint64_t act = bsd::ballot(i < nquery);
+            const uint64_t in = h.contains_mask(i < nquery ? qkeys[i] : bsd::INVALID, act);
+            if (i < nquery) out_contains[i] = bsw::lane_in(in) ? 1u : 0u;
+        }
     } else {
         bsd::BloomLds f;
         f.w = reinterpret_cast<uint32_t*>(smem);

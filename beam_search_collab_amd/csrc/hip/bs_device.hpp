@@ -406,14 +406,14 @@ struct HashLds {
         for (uint32_t base = 0; base < size; base += 64) {
             const uint32_t off = base + lane;
             const uint32_t idx = add(h, off < size ? off : 0u);
-            const uint32_t s = (off < size) ? t[idx] : 0u;
-            const uint64_t hit = ballot(off < size && s == k);
-            const uint64_t emp = ballot(off < size && s == INVALID);
-            const uint64_t any = hit | emp;
+            const uint32_t s = t[idx];  // lanes past the table read the home slot, masked below
+            const uint64_t in = size - base >= 64u ? ~0ull : (1ull << (size - base)) - 1ull;
+            const uint64_t hit = ballot(s == k) & in;
+            const uint64_t any = hit | (ballot(s == INVALID) & in);
             if (any) {
                 const uint32_t first = static_cast<uint32_t>(__builtin_ctzll(any));
                 if ((hit >> first) & 1ull) return 0u;
-                if (lane == first) t[idx] = k;
+                if (bsw::lane_in(1ull << first)) t[idx] = k;
                 wave_sync();
                 occ += 1;
                 return 1u;
@@ -422,26 +422,34 @@ struct HashLds {
         return 0u;
     }
 
-    __device__ __forceinline__ bool contains_lane(uint32_t k) const {
+    // Lanes of `active` whose key is in the table.  Every lane of the wave takes part: the
+    // probe runs group by group for the whole wave, with the lanes still searching kept in
+    // a mask, until each of them has met its key or an empty slot.  A key's sequence starts
+    // at its home slot: the slots before it in its group of 4 are not in the sequence (they
+    // end it, after a full turn).
+    __device__ __forceinline__ uint64_t contains_mask(uint32_t k, uint64_t active) const {
+        const uint4* t4 = reinterpret_cast<const uint4*>(t);
         const uint32_t s0 = home(k);
         const uint32_t nq = size >> 2;
         uint32_t q = s0 >> 2;
-        // the slots before the home slot in its group of 4 are not in k's sequence (they
-        // end it, after a full turn)
         const uint32_t f = s0 & 3u;
-        uint4 v = reinterpret_cast<const uint4*>(t)[q];
-        bool hit = (v.x == k && f == 0) || (v.y == k && f <= 1) || (v.z == k && f <= 2) || v.w == k;
-        bool emp = (v.x == INVALID && f == 0) || (v.y == INVALID && f <= 1) || (v.z == INVALID && f <= 2) ||
-                   v.w == INVALID;
-        for (uint32_t i = 0; i < nq; ++i) {
-            if (hit) return true;
-            if (emp) return false;
+        const uint64_t f0 = ballot(f == 0u), f1 = ballot(f <= 1u), f2 = ballot(f <= 2u);
+        uint4 v = t4[q];
+        uint64_t hit = (ballot(v.x == k) & f0) | (ballot(v.y == k) & f1) | (ballot(v.z == k) & f2) | ballot(v.w == k);
+        const uint64_t emp = (ballot(v.x == INVALID) & f0) | (ballot(v.y == INVALID) & f1) |
+                             (ballot(v.z == INVALID) & f2) | ballot(v.w == INVALID);
+        uint64_t found = hit & active;
+        uint64_t pending = active & ~(hit | emp);
+        for (uint32_t i = 0; pending != 0 && i < nq; ++i) {
             q = q + 1 == nq ? 0u : q + 1;
-            v = reinterpret_cast<const uint4*>(t)[q];
-            hit = v.x == k || v.y == k || v.z == k || v.w == k;
-            emp = v.x == INVALID || v.y == INVALID || v.z == INVALID || v.w == INVALID;
+            v = t4[q];
+            hit = ballot(v.x == k) | ballot(v.y == k) | ballot(v.z == k) | ballot(v.w == k);
+            // INVALID is the largest word: a group holds an empty slot iff its maximum is INVALID
+            const uint64_t e = ballot(max(max(v.x, v.y), max(v.z, v.w)) == INVALID);
+            found |= hit & pending;
+            pending &= ~(hit | e);
         }
-        return hit;
+        return found;
     }
 
     // lane-parallel batch (one key per lane, INVALID = idle).  Sequential semantics in

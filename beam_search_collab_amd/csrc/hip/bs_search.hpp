@@ -353,10 +353,11 @@ search_kernel(const SearchParams p) {
 #pragma unroll
             for (int rc = 0; rc < CR; ++rc) {
                 const uint32_t i = static_cast<uint32_t>(rc) * 64u + lane;
-                const bool valid = i < p.R && child[rc] != INVALID && !hf.contains_lane(child[rc]);
+                uint64_t ok = ballot(i < p.R && child[rc] != INVALID);
+                ok &= ~hf.contains_mask(child[rc], ok);
                 const float est = estimate(raw[rc], qo.sum_q, qo.width, qo.low, ftx[rc], ffd[rc], ffv[rc], exact);
-                ck[rc] = valid ? make_key(est, child[rc]) : EMPTY_KEY;
-                cm[rc] = ballot(valid);
+                ck[rc] = bsw::lane_in(ok) ? make_key(est, child[rc]) : EMPTY_KEY;
+                cm[rc] = ok;
                 nv += static_cast<uint32_t>(__builtin_popcountll(cm[rc]));
             }
             wave_sync();
