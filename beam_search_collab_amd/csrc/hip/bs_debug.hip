@@ -218,7 +218,7 @@ __global__ void __launch_bounds__(64) dbg_beam_kernel(uint32_t T, const uint64_t
     uint64_t beam[TR];
 #pragma unroll
     for (int r = 0; r < TR; ++r) beam[r] = bsd::EMPTY_KEY;
-    uint32_t first = 0;  // the pick's scan start (maintained by merge and pick)
+    bsd::BeamState st = {0u, bsd::EMPTY_KEY};  // kept by merge and pick
     for (uint32_t b = 0; b < nbatch; ++b) {
         uint64_t ck[CR], cm[CR];
 #pragma unroll
@@ -227,9 +227,9 @@ __global__ void __launch_bounds__(64) dbg_beam_kernel(uint32_t T, const uint64_t
             ck[rc] = (j < bsize) ? keys[static_cast<uint64_t>(b) * bsize + j] : bsd::EMPTY_KEY;
             cm[rc] = bsd::ballot(ck[rc] != bsd::EMPTY_KEY);
         }
-        bsd::beam_merge<TR, CR>(beam, ck, cm, T, scratch, scratch + 64 * TR + 2, &first);
+        bsd::beam_merge<TR, CR>(beam, ck, cm, T, scratch, scratch + 64 * TR + 2, st);
         for (uint32_t k = 0; k < picks; ++k) {
-            const uint32_t id = bsd::beam_pick<TR, RUN>(beam, first);
+            const uint32_t id = bsd::beam_pick<TR, RUN>(beam, st);
             if (lane == 0) picked[static_cast<uint64_t>(b) * picks + k] = id;
         }
     }

@@ -54,20 +54,60 @@ __device__ __forceinline__ uint32_t key_id(uint64_t k) { return static_cast<uint
 // These positions are a permutation of 0..T+c-1; the first T form the new beam.
 // A candidate whose key is >= the beam's last key (EMPTY while the beam is not full)
 // lands at position >= T and is evicted (ties go after beam entries), so it is dropped
-// first.  Two ways to the same result:
-//  - rank loop: each remaining candidate is broadcast once and compared with every beam
-//    register, ~(3*TR+6) instructions per candidate (few candidates);
+// first.  The beam stays sorted (a mark sets a key's LSB: beam_pick marks the last of a
+// run of identical keys).  Two ways to the same result:
+//  - rank loop: each remaining candidate kj is broadcast once.  The registers whose last
+//    key is <= kj keep their elements, register rs = #(such registers) holds kj's
+//    insertion point (its elements > kj shift by one: one compare), every later register
+//    shifts by one as a whole (a scalar count);
 //  - sorted merge (CR = 1, SORTED, at least merge_sort_min<TR>() candidates): the candidates are
 //    compacted and bitonic-sorted across lanes, each finds its rank in the beam by a
 //    binary search of an LDS copy, the occupied output slots are marked in a bitmap and
 //    every output slot gathers its key from the candidate or the beam copy.
 // Identical keys are indistinguishable, so the two orders of equal candidates agree.
-// Both loops use the sorted merge for one candidate register (degree <= 64); the kernels
-// that would lose a wavefront per SIMD to its registers are compiled for 5 waves per SIMD.
 // LDS: scratch = 64*TR + 1 keys (the last one a dump slot), aux = 64 + TR keys.
 // ---------------------------------------------------------------------------
-// The rank loop costs ~(9 + 2 TR) instructions per candidate, the sorted merge a roughly
-// fixed ~250 plus LDS latency: the crossover falls with the beam size.
+// What merge and pick keep besides the registers: `first`, a lower bound on the register
+// that holds the first unexpanded key (0 always is one), and `last`, lane r < TR holding
+// the last key of register r (element 64 r + 63), EMPTY in the lanes beyond.
+struct BeamState {
+    uint32_t first;
+    uint64_t last;
+};
+
+template <int TR>
+__device__ __forceinline__ BeamState beam_state(const uint64_t (&beam)[TR]) {
+    BeamState st;
+    st.first = 0;
+    st.last = EMPTY_KEY;
+#pragma unroll
+    for (int r = 0; r < TR; ++r) st.last = bsw::lane_in(1ull << r) ? readlane64(beam[r], 63) : st.last;
+    return st;
+}
+
+// register r of the beam (wave-uniform r: a register-indexed move, s_set_gpr_idx)
+template <int TR>
+__device__ __forceinline__ uint64_t beam_reg(const uint64_t (&beam)[TR], uint32_t r) {
+    return beam[r];
+}
+
+// lanes r < TR whose register's last slot 64 r + 63 lies below T
+template <int TR>
+__device__ __forceinline__ uint64_t last_live(uint32_t T) {
+    const uint32_t full = T >> 6;  // registers with every slot below T
+    const uint32_t n = full < static_cast<uint32_t>(TR) ? full : static_cast<uint32_t>(TR);
+    return n >= 64u ? ~0ull : (1ull << n) - 1ull;
+}
+
+// The rank loop finds a candidate's register from the registers' last keys (beams of 12
+// or more registers; ~8 instructions per candidate, plus the last keys' upkeep) or by
+// comparing it with every register (smaller beams; ~2 TR + 6).  The sorted merge's fixed
+// cost (~250 instructions plus LDS latency) against the rank loop's: the crossover.
+template <int TR>
+__device__ __forceinline__ constexpr bool merge_split() {
+    return TR >= 12;
+}
+
 template <int TR>
 __device__ __forceinline__ constexpr uint32_t merge_sort_min() {
     return TR >= 16 ? 3u : TR >= 8 ? 5u : 8u;
@@ -117,7 +157,7 @@ __device__ __forceinline__ uint64_t sort_lanes(uint64_t v, uint32_t n) {
 
 template <int TR>
 __device__ __forceinline__ void beam_merge_sorted(uint64_t (&beam)[TR], uint64_t ck, uint64_t cmask, uint32_t n,
-                                                  uint32_t T, uint64_t* B, uint64_t* aux, uint32_t* first) {
+                                                  uint32_t T, uint64_t* B, uint64_t* aux, BeamState& st) {
     const uint32_t lane = lane_id();
     uint64_t* C = aux;       // 64 sorted candidates
     uint64_t* M = aux + 64;  // TR words: bit s = output slot s holds a candidate
@@ -138,7 +178,7 @@ __device__ __forceinline__ void beam_merge_sorted(uint64_t (&beam)[TR], uint64_t
     for (uint32_t step = 32; step >= 1; step >>= 1)
         if (B[lo + step - 1] <= c) lo += step;
     const uint32_t pos = lane + lo;
-    if (first) *first = min(*first, uniform(pos) >> 6);  // lane 0: the smallest candidate
+    st.first = min(st.first, uniform(pos) >> 6);  // lane 0: the smallest candidate
     C[lane] = c;  // sorted (EMPTY past n)
     {
         // every lane ors a word (0 unless it places a candidate): no divergent branch
@@ -160,15 +200,24 @@ __device__ __forceinline__ void beam_merge_sorted(uint64_t (&beam)[TR], uint64_t
         before += static_cast<uint32_t>(__builtin_popcountll(mw));
     }
     beam_clear_tail<TR>(beam, T);
+    if constexpr (merge_split<TR>()) {
+        // the registers' last keys into lanes 0..TR-1, through C (free once gathered; the
+        // wave's LDS accesses complete in order)
+        if (lane == 63u) {
+#pragma unroll
+            for (int r = 0; r < TR; ++r) C[r] = beam[r];
+        }
+        wave_sync();
+        const uint64_t lk = C[lane < static_cast<uint32_t>(TR) ? lane : 0u];
+        st.last = lane < static_cast<uint32_t>(TR) ? lk : EMPTY_KEY;
+    }
     wave_sync();
 }
 
-// first (optional): the pick's lower bound on the register of the first unexpanded key,
-// lowered to the register where the smallest candidate lands.
 template <int TR, int CR, bool SORTED = true>
 __device__ __forceinline__ void beam_merge(uint64_t (&beam)[TR], const uint64_t (&ck)[CR],
                                            const uint64_t (&cmask_in)[CR], uint32_t T,
-                                           uint64_t* lds_scratch, uint64_t* lds_aux, uint32_t* first = nullptr) {
+                                           uint64_t* lds_scratch, uint64_t* lds_aux, BeamState& st) {
     const uint32_t lane = lane_id();
     const uint64_t thr = readlane64(beam[(T - 1) >> 6], (T - 1) & 63u);
     uint64_t cmask[CR];
@@ -181,13 +230,19 @@ __device__ __forceinline__ void beam_merge(uint64_t (&beam)[TR], const uint64_t 
     if (n == 0) return;
     if constexpr (CR == 1 && SORTED) {
         if (n >= merge_sort_min<TR>()) {
-            beam_merge_sorted<TR>(beam, ck[0], cmask[0], n, T, lds_scratch, lds_aux, first);
+            beam_merge_sorted<TR>(beam, ck[0], cmask[0], n, T, lds_scratch, lds_aux, st);
             return;
         }
     }
-    uint32_t bpos[TR];
+    constexpr bool SPLIT = merge_split<TR>();
+    // lp[r]: per-lane shift of register r (SPLIT: by the candidates whose insertion point is
+    // inside it; otherwise: by every smaller candidate); nsplit (SPLIT): 8-bit counts of
+    // those candidates per register (registers 0-7, 8-15), from which the later registers'
+    // whole-register shifts follow
+    uint32_t lp[TR];
 #pragma unroll
-    for (int r = 0; r < TR; ++r) bpos[r] = static_cast<uint32_t>(r) * 64u + lane;
+    for (int r = 0; r < TR; ++r) lp[r] = 0;
+    uint64_t nsplit0 = 0, nsplit1 = 0;
     uint32_t cpos[CR];
 #pragma unroll
     for (int rc = 0; rc < CR; ++rc) cpos[rc] = 0;
@@ -200,12 +255,25 @@ __device__ __forceinline__ void beam_merge(uint64_t (&beam)[TR], const uint64_t 
             const uint32_t lj = static_cast<uint32_t>(__builtin_ctzll(m));
             m &= m - 1;
             const uint64_t kj = readlane64(ck[rj], lj);
-            uint32_t le = 0;
+            uint32_t le;  // #(beam <= kj)
+            if constexpr (SPLIT) {
+                // kj < thr: register (T - 1) / 64 ends above kj, so rs < TR
+                const uint32_t rs = static_cast<uint32_t>(__builtin_popcountll(ballot(st.last <= kj)));
+                const uint64_t lt = ballot(kj < beam_reg<TR>(beam, rs));
+                lp[rs] += bsw::lane_in(lt) ? 1u : 0u;
+                const uint64_t inc = 1ull << (8u * (rs & 7u));
+                nsplit0 += rs < 8u ? inc : 0ull;
+                nsplit1 += rs < 8u ? 0ull : inc;
+                le = 64u * rs + static_cast<uint32_t>(__builtin_popcountll(~lt));
+            } else {
+                uint32_t ngt = 0;
 #pragma unroll
-            for (int r = 0; r < TR; ++r) {
-                const bool lt = kj < beam[r];
-                bpos[r] += lt ? 1u : 0u;
-                le += static_cast<uint32_t>(__builtin_popcountll(~ballot(lt)));
+                for (int r = 0; r < TR; ++r) {
+                    const uint64_t lt = ballot(kj < beam[r]);
+                    lp[r] += bsw::lane_in(lt) ? 1u : 0u;
+                    ngt += static_cast<uint32_t>(__builtin_popcountll(lt));
+                }
+                le = 64u * TR - ngt;
             }
             minle = min(minle, le);
 #pragma unroll
@@ -223,15 +291,25 @@ __device__ __forceinline__ void beam_merge(uint64_t (&beam)[TR], const uint64_t 
     // keys landing at 64*TR or beyond go to the dump slot 64*TR, those landing in
     // [T, 64*TR) are overwritten with EMPTY after the gather (beam_clear_tail).
     constexpr uint32_t DUMP = 64u * TR;
+    uint32_t shift = 0;  // candidates inserted in earlier registers
 #pragma unroll
-    for (int r = 0; r < TR; ++r) lds_scratch[min(bpos[r], DUMP)] = beam[r];
+    for (int r = 0; r < TR; ++r) {
+        const uint32_t bpos = static_cast<uint32_t>(r) * 64u + shift + lane + lp[r];
+        lds_scratch[min(bpos, DUMP)] = beam[r];
+        shift += static_cast<uint32_t>(((r < 8 ? nsplit0 : nsplit1) >> (8 * (r & 7))) & 0xFFu);
+    }
 #pragma unroll
     for (int rc = 0; rc < CR; ++rc) lds_scratch[bsw::lane_in(cmask[rc]) ? min(cpos[rc], DUMP) : DUMP] = ck[rc];
     wave_sync();
 #pragma unroll
     for (int r = 0; r < TR; ++r) beam[r] = lds_scratch[static_cast<uint32_t>(r) * 64u + lane];
+    if constexpr (SPLIT) {
+        // lane r: slot 64 r + 63 (EMPTY at T and beyond)
+        const uint64_t lk = lds_scratch[min(64u * lane + 63u, DUMP)];
+        st.last = bsw::lane_in(last_live<TR>(T)) ? lk : EMPTY_KEY;
+    }
     beam_clear_tail<TR>(beam, T);
-    if (first) *first = min(*first, minle >> 6);
+    st.first = min(st.first, minle >> 6);
     wave_sync();
 }
 
@@ -240,24 +318,18 @@ __device__ __forceinline__ void beam_merge(uint64_t (&beam)[TR], const uint64_t 
 // id (INVALID if none).  RUN = true (the rabitq beam may hold identical keys): of a run
 // of identical keys the last one is marked, which keeps the beam sorted.
 // ---------------------------------------------------------------------------
-// register r of the beam (wave-uniform r: a register-indexed move, s_set_gpr_idx)
-template <int TR>
-__device__ __forceinline__ uint64_t beam_reg(const uint64_t (&beam)[TR], uint32_t r) {
-    return beam[r];
-}
 
-// first: a lower bound on the register that holds the first unexpanded key (0 always is
-// one).  Keys only move to later slots, so the bound holds until a merge places a
+// st.first: keys only move to later slots, so the bound holds until a merge places a
 // candidate before it (beam_merge lowers it); the pick scans from it and leaves it at the
 // register where it found its key.
 template <int TR, bool RUN>
-__device__ __forceinline__ uint32_t beam_pick(uint64_t (&beam)[TR], uint32_t& first) {
+__device__ __forceinline__ uint32_t beam_pick(uint64_t (&beam)[TR], BeamState& st) {
     // the first register holding an unexpanded key, its first such lane
-    uint32_t pr = first;
+    uint32_t pr = st.first;
     uint64_t row, mp;
     for (;;) {
         if (pr >= static_cast<uint32_t>(TR)) {
-            first = pr;
+            st.first = pr;
             return INVALID;
         }
         row = beam_reg<TR>(beam, pr);
@@ -265,7 +337,7 @@ __device__ __forceinline__ uint32_t beam_pick(uint64_t (&beam)[TR], uint32_t& fi
         if (mp != 0) break;
         ++pr;
     }
-    first = pr;
+    st.first = pr;
     const uint32_t pl = static_cast<uint32_t>(__builtin_ctzll(mp));
     const uint64_t kp = readlane64(row, pl);
     uint32_t qr = pr, ql = pl;
@@ -287,6 +359,7 @@ __device__ __forceinline__ uint32_t beam_pick(uint64_t (&beam)[TR], uint32_t& fi
     }
     // set the mark (key LSB) of element (qr, ql)
     beam[qr] |= bsw::lane_in(1ull << ql) ? 1ull : 0ull;
+    if constexpr (merge_split<TR>()) st.last |= bsw::lane_in(ql == 63u ? 1ull << qr : 0ull) ? 1ull : 0ull;
     return key_id(kp);
 }
 

@@ -145,10 +145,11 @@ __global__ void __launch_bounds__(256) gt_select(const float* vecs, uint32_t dst
                 }
                 written |= 1u << i;
                 // one HBM round trip of the list per flush, then the buffer in runs of 64
+                bsd::BeamState st = bsd::beam_state<2>(beam);
                 for (uint32_t b0 = 0; b0 < c; b0 += 64) {
                     uint64_t ck[1] = {b0 + lane < c ? buf[i * BUF + b0 + lane] : EMPTY_KEY};
                     uint64_t cm[1] = {ballot(b0 + lane < c)};
-                    bsd::beam_merge<2, 1, true>(beam, ck, cm, C, mscr, maux);
+                    bsd::beam_merge<2, 1, true>(beam, ck, cm, C, mscr, maux, st);
                 }
                 top[lane] = beam[0];
                 top[64 + lane] = beam[1];
@@ -261,10 +262,11 @@ __global__ void __launch_bounds__(256) gt_refine(const float* vecs, uint32_t dst
 
     const uint64_t* lists = topc + qi * nsplit * C;
     uint64_t beam[2] = {lists[lane], lists[64 + lane]};
+    bsd::BeamState st = bsd::beam_state<2>(beam);
     for (uint32_t s = 1; s < nsplit; ++s) {
         uint64_t ck[2] = {lists[s * C + lane], lists[s * C + 64 + lane]};
         uint64_t cm[2] = {ballot(ck[0] != EMPTY_KEY), ballot(ck[1] != EMPTY_KEY)};
-        bsd::beam_merge<2, 2, false>(beam, ck, cm, C, mscr, maux);
+        bsd::beam_merge<2, 2, false>(beam, ck, cm, C, mscr, maux, st);
     }
     const uint64_t kc = readlane64(beam[1], 63);  // the C-th approximate key
 

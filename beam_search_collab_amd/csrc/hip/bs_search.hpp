@@ -84,7 +84,7 @@ search_kernel(const SearchParams p) {
     for (int r = 0; r < TR; ++r) beam[r] = EMPTY_KEY;
 
     uint32_t n_iter = 0, n_exp = 0, n_dist = 0, n_est = 0, n_rr = 0;
-    uint32_t first = 0;  // lower bound on the beam register of the first unexpanded key
+    BeamState st = {0u, EMPTY_KEY};  // the pick's scan start, the registers' last keys
 
     if constexpr (MODE == MODE_HASH || MODE == MODE_BLOOM) {
         // ------------------------------------------------------------------ base
@@ -147,7 +147,7 @@ search_kernel(const SearchParams p) {
             bool any = false;
 #pragma unroll
             for (int rc = 0; rc < CR; ++rc) any = any || (cm[rc] != 0);
-            if (any) beam_merge<TR, CR, (CR == 1)>(beam, ck, cm, T, scratch, merge_aux, &first);
+            if (any) beam_merge<TR, CR, (CR == 1)>(beam, ck, cm, T, scratch, merge_aux, st);
 #pragma unroll
             for (int rc = 0; rc < CR; ++rc) cm[rc] = 0;
 
@@ -175,7 +175,7 @@ search_kernel(const SearchParams p) {
             }
 
             // pick the best unexpanded node
-            const uint32_t parent = beam_pick<TR, false>(beam, first);
+            const uint32_t parent = beam_pick<TR, false>(beam, st);
             if (parent == INVALID) break;
             ++n_exp;
 
@@ -230,7 +230,7 @@ search_kernel(const SearchParams p) {
             bool any = false;
 #pragma unroll
             for (int rc = 0; rc < CR; ++rc) any = any || (cm[rc] != 0);
-            if (any) beam_merge<TR, CR, (CR == 1)>(beam, ck, cm, T, scratch, merge_aux);
+            if (any) beam_merge<TR, CR, (CR == 1)>(beam, ck, cm, T, scratch, merge_aux, st);
         }
         // flush the K smallest, ascending
         uint32_t* out = p.results + qid * p.K;
@@ -278,13 +278,13 @@ search_kernel(const SearchParams p) {
             n_dist = 1;
             uint64_t ck[1] = {lane == 0 ? make_key(d0, p.entry) : EMPTY_KEY};
             uint64_t cm[1] = {1ull};
-            beam_merge<TR, 1>(beam, ck, cm, T, scratch, merge_aux);
+            beam_merge<TR, 1>(beam, ck, cm, T, scratch, merge_aux, st);
         }
         uint32_t* rawbuf = cand_ids;
 
         for (int32_t iter = 0; iter < p.max_it; ++iter) {
             ++n_iter;
-            const uint32_t parent = beam_pick<TR, true>(beam, first);
+            const uint32_t parent = beam_pick<TR, true>(beam, st);
             if (parent == INVALID) break;
             if (!hf.insert1(parent)) continue;  // already expanded (gpu_search_rabitq.cuh:249-252)
             ++n_exp;
@@ -362,7 +362,7 @@ search_kernel(const SearchParams p) {
             }
             wave_sync();
             n_est += nv;
-            beam_merge<TR, CR>(beam, ck, cm, T, scratch, merge_aux, &first);
+            beam_merge<TR, CR>(beam, ck, cm, T, scratch, merge_aux, st);
         }
 
         // exact rerank of every beam slot (gpu_search_rabitq.cuh:314-317)
