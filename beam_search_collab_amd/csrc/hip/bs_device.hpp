@@ -322,8 +322,10 @@ __device__ __forceinline__ void beam_merge(uint64_t (&beam)[TR], const uint64_t 
 // st.first: keys only move to later slots, so the bound holds until a merge places a
 // candidate before it (beam_merge lowers it); the pick scans from it and leaves it at the
 // register where it found its key.
+// next_key (optional): the unexpanded key that follows the picked one in the beam
+// (EMPTY_KEY if none), for a prediction of the following pick.
 template <int TR, bool RUN>
-__device__ __forceinline__ uint32_t beam_pick(uint64_t (&beam)[TR], BeamState& st) {
+__device__ __forceinline__ uint32_t beam_pick(uint64_t (&beam)[TR], BeamState& st, uint64_t* next_key = nullptr) {
     // the first register holding an unexpanded key, its first such lane
     uint32_t pr = st.first;
     uint64_t row, mp;
@@ -340,6 +342,23 @@ __device__ __forceinline__ uint32_t beam_pick(uint64_t (&beam)[TR], BeamState& s
     st.first = pr;
     const uint32_t pl = static_cast<uint32_t>(__builtin_ctzll(mp));
     const uint64_t kp = readlane64(row, pl);
+    if (next_key) {
+        uint64_t nk = EMPTY_KEY;
+        const uint64_t mp2 = mp & (mp - 1u);
+        if (mp2 != 0) {
+            nk = readlane64(row, static_cast<uint32_t>(__builtin_ctzll(mp2)));
+        } else {
+            for (uint32_t r = pr + 1; r < static_cast<uint32_t>(TR); ++r) {
+                const uint64_t row2 = beam_reg<TR>(beam, r);
+                const uint64_t m2 = ballot((static_cast<uint32_t>(row2) & 1u) == 0u);
+                if (m2 != 0) {
+                    nk = readlane64(row2, static_cast<uint32_t>(__builtin_ctzll(m2)));
+                    break;
+                }
+            }
+        }
+        *next_key = nk;
+    }
     uint32_t qr = pr, ql = pl;
     if constexpr (RUN) {
         // identical keys are rare: look at the next element first, scan only if it repeats
@@ -361,6 +380,26 @@ __device__ __forceinline__ uint32_t beam_pick(uint64_t (&beam)[TR], BeamState& s
     beam[qr] |= bsw::lane_in(1ull << ql) ? 1ull : 0ull;
     if constexpr (merge_split<TR>()) st.last |= bsw::lane_in(ql == 63u ? 1ull << qr : 0ull) ? 1ull : 0ull;
     return key_id(kp);
+}
+
+// The smallest key held by the lanes of k[0..CR) (EMPTY_KEY if none), for the prediction
+// of the next pick: after a merge the smallest unexpanded key is the smaller of the beam's
+// next unexpanded key (beam_pick's next_key) and the smallest merged candidate.  The upper
+// words are reduced exactly; among keys sharing the smallest upper word the lowest lane's
+// is returned.
+template <int CR>
+__device__ __forceinline__ uint64_t wave_min_key(const uint64_t (&k)[CR]) {
+    uint64_t v = k[0];
+#pragma unroll
+    for (int rc = 1; rc < CR; ++rc) v = k[rc] < v ? k[rc] : v;
+    const uint32_t vh = static_cast<uint32_t>(v >> 32);
+    uint32_t h = vh;
+    h = min(h, bsw::xor_lane<1>(h));
+    h = min(h, bsw::xor_lane<2>(h));
+    h = min(h, bsw::xor_lane<4>(h));
+    h = min(h, bsw::xor_lane<8>(h));
+    const uint32_t m = min(min(readlane(h, 0), readlane(h, 16)), min(readlane(h, 32), readlane(h, 48)));
+    return readlane64(v, static_cast<uint32_t>(__builtin_ctzll(ballot(vh == m))));
 }
 
 // ---------------------------------------------------------------------------

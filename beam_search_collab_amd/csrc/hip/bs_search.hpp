@@ -140,6 +140,13 @@ search_kernel(const SearchParams p) {
             }
         }
         int32_t until_reset = p.reset;
+        // The neighbour list of the predicted next parent is requested before the merge,
+        // so its HBM round trip overlaps merge, refill and pick: after the merge the
+        // smallest unexpanded key is the smaller of the beam's next unexpanded key and the
+        // smallest merged candidate.  The list is used only when the pick returns that node.
+        uint32_t pre = INVALID;
+        uint32_t pre_child[CR];
+        uint64_t next_key = EMPTY_KEY;
 
         for (int32_t iter = 0; iter < p.max_it; ++iter) {
             ++n_iter;
@@ -175,17 +182,27 @@ search_kernel(const SearchParams p) {
             }
 
             // pick the best unexpanded node
-            const uint32_t parent = beam_pick<TR, false>(beam, st);
+            const uint32_t parent = beam_pick<TR, false>(beam, st, &next_key);
             if (parent == INVALID) break;
             ++n_exp;
 
             // expand: neighbours through the filter
-            const uint32_t* row = p.edges + static_cast<uint64_t>(parent) * p.R;
             uint32_t child[CR], isnew[CR];
+            if (parent == pre) {
+#pragma unroll
+                for (int rc = 0; rc < CR; ++rc) child[rc] = pre_child[rc];
+            } else {
+                const uint32_t* row = p.edges + static_cast<uint64_t>(parent) * p.R;
+#pragma unroll
+                for (int rc = 0; rc < CR; ++rc) {
+                    const uint32_t i = static_cast<uint32_t>(rc) * 64u + lane;
+                    child[rc] = row[i < p.R ? i : 0u];
+                }
+            }
 #pragma unroll
             for (int rc = 0; rc < CR; ++rc) {
                 const uint32_t i = static_cast<uint32_t>(rc) * 64u + lane;
-                child[rc] = (i < p.R) ? row[i] : INVALID;
+                child[rc] = (i < p.R) ? child[rc] : INVALID;
             }
             if constexpr (MODE == MODE_HASH) {
 #pragma unroll
@@ -221,6 +238,19 @@ search_kernel(const SearchParams p) {
                 cm[rc] = ballot(v);
             }
             wave_sync();
+            {
+                const uint64_t c0 = wave_min_key<CR>(ck);
+                const uint64_t nk = c0 < next_key ? c0 : next_key;
+                pre = nk == EMPTY_KEY ? INVALID : key_id(nk);
+                if (pre != INVALID) {
+                    const uint32_t* row = p.edges + static_cast<uint64_t>(pre) * p.R;
+#pragma unroll
+                    for (int rc = 0; rc < CR; ++rc) {
+                        const uint32_t i = static_cast<uint32_t>(rc) * 64u + lane;
+                        pre_child[rc] = row[i < p.R ? i : 0u];
+                    }
+                }
+            }
         }
         if (coop > 1) {  // release the helper wavefronts
             if (lane == 0) *batch = INVALID;
