@@ -165,7 +165,7 @@ extern "C" int bs_index_create(const float* vecs, const uint32_t* edges, uint64_
     if (!vecs || !edges) return fail(BS_EINVAL, "vecs and edges must be given");
     if (n == 0 || n > 0x7FFFFFFFull) return fail(BS_EINVAL, "need 0 < n < 2^31");
     if (dim == 0 || dim > 1024) return fail(BS_EINVAL, "dim must be in 1..1024");
-    if (degree == 0 || degree > 128) return fail(BS_EINVAL, "degree must be in 1..128");
+    if (degree == 0 || degree > 256) return fail(BS_EINVAL, "degree must be in 1..256");
     // every neighbour id must address a node (the kernels gather rows without bounds checks)
     for (uint64_t i = 0, cnt = n * degree; i < cnt; ++i) {
         const uint32_t e = edges[i];
@@ -391,7 +391,7 @@ int make_plan(bs_index ix, const bs_search_cfg* cfg, uint64_t nq, Plan& pl) {
 
     pl.mode = mode;
     pl.TR = T <= 64 ? 1 : T <= 128 ? 2 : T <= 256 ? 4 : T <= 512 ? 8 : (T <= 768 && mode == BS_RABITQ) ? 12 : 16;
-    pl.CR = ix->degree <= 64 ? 1 : 2;
+    pl.CR = ix->degree <= 64 ? 1 : ix->degree <= 128 ? 2 : 4;
     bsd::L2Shape L = bsd::l2_shape(ix->dim);
     if (L.QR > 4) return fail(BS_EINVAL, "dim too large");
     pl.PB = bsd::l2_passes_in_flight(L);

@@ -103,9 +103,9 @@ __device__ __forceinline__ uint64_t last_live(uint32_t T) {
 // or more registers; ~8 instructions per candidate, plus the last keys' upkeep) or by
 // comparing it with every register (smaller beams; ~2 TR + 6).  The sorted merge's fixed
 // cost (~250 instructions plus LDS latency) against the rank loop's: the crossover.
-template <int TR>
+template <int TR, int CR>
 __device__ __forceinline__ constexpr bool merge_split() {
-    return TR >= 12;
+    return TR >= 12 && CR <= 3;  // 8-bit split counts: at most 192 candidates
 }
 
 template <int TR>
@@ -200,7 +200,7 @@ __device__ __forceinline__ void beam_merge_sorted(uint64_t (&beam)[TR], uint64_t
         before += static_cast<uint32_t>(__builtin_popcountll(mw));
     }
     beam_clear_tail<TR>(beam, T);
-    if constexpr (merge_split<TR>()) {
+    if constexpr (merge_split<TR, 1>()) {
         // the registers' last keys into lanes 0..TR-1, through C (free once gathered; the
         // wave's LDS accesses complete in order)
         if (lane == 63u) {
@@ -234,7 +234,7 @@ __device__ __forceinline__ void beam_merge(uint64_t (&beam)[TR], const uint64_t 
             return;
         }
     }
-    constexpr bool SPLIT = merge_split<TR>();
+    constexpr bool SPLIT = merge_split<TR, CR>();
     // lp[r]: per-lane shift of register r (SPLIT: by the candidates whose insertion point is
     // inside it; otherwise: by every smaller candidate); nsplit (SPLIT): 8-bit counts of
     // those candidates per register (registers 0-7, 8-15), from which the later registers'
@@ -378,7 +378,7 @@ __device__ __forceinline__ uint32_t beam_pick(uint64_t (&beam)[TR], BeamState& s
     }
     // set the mark (key LSB) of element (qr, ql)
     beam[qr] |= bsw::lane_in(1ull << ql) ? 1ull : 0ull;
-    if constexpr (merge_split<TR>()) st.last |= bsw::lane_in(ql == 63u ? 1ull << qr : 0ull) ? 1ull : 0ull;
+    if constexpr (merge_split<TR, 1>()) st.last |= bsw::lane_in(ql == 63u ? 1ull << qr : 0ull) ? 1ull : 0ull;
     return key_id(kp);
 }
 

@@ -45,7 +45,10 @@ static hipError_t launch_p(const SearchParams& p, int PB, dim3 g, dim3 b, size_t
 template <int TR>
 static hipError_t launch_c(const SearchParams& p, int CR, int PB, dim3 g, dim3 b, size_t lds, hipStream_t s,
                            int* occ) {
-    return CR == 1 ? launch_p<TR, 1>(p, PB, g, b, lds, s, occ) : launch_p<TR, 2>(p, PB, g, b, lds, s, occ);
+    // degree <= 64, <= 128, <= 256 (gpu_cli.cu:208-233)
+    return CR == 1   ? launch_p<TR, 1>(p, PB, g, b, lds, s, occ)
+           : CR == 2 ? launch_p<TR, 2>(p, PB, g, b, lds, s, occ)
+                     : launch_p<TR, 4>(p, PB, g, b, lds, s, occ);
 }
 
 static hipError_t launch_any(const SearchParams& p, int TR, int CR, int PB, dim3 g, dim3 b, size_t lds,

@@ -57,12 +57,18 @@ typedef struct {
     int32_t mode;               /* bs_mode                                             */
     uint32_t queries_per_group; /* wavefronts (queries) per workgroup: 1,2,4,8; 0 -> 1  */
     uint32_t K;                 /* results per query (>= 1, <= topk_size)              */
-    uint32_t topk_size;         /* beam slots, 1..1024                                 */
+    uint32_t topk_size;         /* beam slots, 1..1024 (see the limits below)          */
     uint32_t filter_capacity;   /* hash slots / Bloom bits (rounded up to a power of 2)*/
     uint32_t entry_point;       /* start node (< n)                                    */
     int32_t max_iterations;     /* >= 0                                                */
     int32_t reset_interval;     /* forgettable-filter reset period; 0 = never (>= 0)   */
 } bs_search_cfg;
+
+/* Limits against the reference: degree 1..256 and dim 1..1024 as gpu_cli (gpu_cli.cu:208-233,
+ * 340-347).  topk_size 1..1024: the beam is held in at most 16 registers of 64 keys per
+ * wavefront (and the RaBitQ expanded set in the wavefront's LDS slice); the reference's
+ * SharedBitonicTopK takes any multiple of 32 in shared memory (topk_shared.cuh:272-331).
+ * Larger beams are refused with BS_EINVAL rather than run slowly from LDS. */
 
 /* Work counters summed over the queries of one call (the byte model of the roofline:
  * base  B_q = 4d + E*4R + D*4d + 4K;
@@ -78,7 +84,7 @@ typedef struct {
 
 /* Upload a graph: vecs n*dim f32, edges n*degree u32 (ids < n or 0xFFFFFFFF).
  * Replaces GPUGraph(const CPUGraph&) (gpu_graph.cuh:81-146).  Validates every edge on
- * the host.  dim 1..1024, degree 1..128, n < 2^31. */
+ * the host.  dim 1..1024, degree 1..256 (the reference gpu_cli's range), n < 2^31. */
 int bs_index_create(const float* vecs, const uint32_t* edges, uint64_t n, uint32_t dim,
                     uint32_t degree, bs_index* out);
 

@@ -52,7 +52,7 @@ def test_argument_errors_before_any_device_call():
     assert b"vecs and edges" in lib.bs_last_error()
     assert lib.bs_index_create(vecs, edges, 2, 0, 2, C.byref(h)) == -1
     assert b"dim" in lib.bs_last_error()
-    assert lib.bs_index_create(vecs, edges, 2, 4, 200, C.byref(h)) == -1
+    assert lib.bs_index_create(vecs, edges, 2, 4, 257, C.byref(h)) == -1
     assert b"degree" in lib.bs_last_error()
     assert lib.bs_index_create(vecs, edges, 2, 4, 2, C.byref(h)) == -1
     assert b"points to node 5" in lib.bs_last_error()

@@ -15,14 +15,14 @@ OMODE = {"base": po.BASE_HASH, "warp": po.BASE_HASH, "bwarp": po.BASE_BLOOM, "ra
 
 
 @functools.lru_cache(maxsize=None)
-def dataset(n, dim, degree, nq, kind="mixture", seed=5):
+def dataset(n, dim, degree, nq, kind="mixture", seed=5, beam=64):
     if kind == "mixture":
         base = host.gen_mixture(n, dim, 16, 0.0, 128.0, 12.0, 0.0, seed, seed + 1)
         q = host.gen_mixture(nq, dim, 16, 0.0, 128.0, 12.0, 0.0, seed, seed + 2)
     else:
         base = host.gen_normalized(n, dim, seed + 1)
         q = host.gen_normalized(nq, dim, seed + 2)
-    edges = host.build_vamana(base, degree, 64, 2.0, 1234, exact=False, threads=0)
+    edges = host.build_vamana(base, degree, beam, 2.0, 1234, exact=False, threads=0)
     erq, codes, factors, signs = host.build_rabitq(base, edges, 12345)
     g = search.GPUGraph(base, edges)
     g.attach_rabitq(codes, factors, signs)
@@ -263,6 +263,20 @@ def test_degree_100_two_candidate_registers(gpu, mode, topk):
     filter's four 32-key rounds; cap 1024 at reset 16 makes Bloom false positives common"""
     ds = dataset(2500, 64, 100, 40, "normalized")
     assert_same(*run_both(ds, mode, 10, topk), f"{mode} R=100 topk={topk}")
+
+
+@pytest.mark.parametrize("degree,dim", [(200, 64), (256, 48), (200, 160)])
+@pytest.mark.parametrize("mode", ["base", "warp2", "bwarp1", "rabitq"])
+def test_degree_above_128_four_candidate_registers(gpu, degree, dim, mode):
+    """degrees 129..256 (the reference gpu_cli's range, gpu_cli.cu:208-233): four candidate
+    registers, the Bloom filter's eight 32-key rounds, rabitq with narrow (dim <= 128) and
+    wide codes (dim 160); beams of two, four and twelve registers"""
+    ds = dataset(1800, dim, degree, 24, "normalized", beam=256)
+    assert int((ds["edges"] != po.INVALID_ID).sum(1).max()) > 128  # rows really use the range
+    for topk in (128, 256, 768):
+        if topk == 768 and mode != "rabitq":
+            continue
+        assert_same(*run_both(ds, mode, 10, topk), f"{mode} R={degree} d={dim} topk={topk}")
 
 
 @pytest.mark.parametrize("degree", [48, 64, 100])
