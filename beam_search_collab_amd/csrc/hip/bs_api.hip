@@ -63,6 +63,7 @@ struct bs_index_s {
     uint32_t* d_recs = nullptr;
     float* d_signs = nullptr;
     size_t max_lds = 65536;
+    size_t lds_cu = 65536;  // LDS per compute unit (shared by its resident workgroups)
     uint32_t cus = 256;  // compute units of the device
     uint32_t xcds = 1;   // XCDs of the device (workgroup b runs on XCD b mod xcds)
     // query scheduling (bs_order.hip): pivots, labels, launch map, for up to ORDER_CHUNK
@@ -80,6 +81,9 @@ struct bs_index_s {
 namespace {
 constexpr uint64_t ORDER_CHUNK = 1u << 18;  // queries per ordered search launch
 constexpr uint64_t ORDER_MIN_NQ = 4096;     // mode 1 orders launches of at least this many
+// LDS is handed to workgroups in 512-B granules (measured on gfx950: a 10848-B workgroup
+// is resident 14 times per CU, not the 15 that 160 KB / 10848 B suggests)
+constexpr uint32_t LDS_GRANULE = 512;
 
 // Pivots for query scheduling: ORDER_P rows spread evenly over the index (all rows when
 // n is smaller), re-ordered by a greedy nearest-neighbour tour so that consecutive
@@ -186,6 +190,9 @@ extern "C" int bs_index_create(const float* vecs, const uint32_t* edges, uint64_
     int lds = 0;
     if (hipDeviceGetAttribute(&lds, hipDeviceAttributeMaxSharedMemoryPerBlock, ix->device) == hipSuccess && lds > 0)
         ix->max_lds = static_cast<size_t>(lds);
+    if (hipDeviceGetAttribute(&lds, hipDeviceAttributeMaxSharedMemoryPerMultiprocessor, ix->device) == hipSuccess &&
+        lds > 0)
+        ix->lds_cu = static_cast<size_t>(lds);
     int cus = 0;
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, ix->device) == hipSuccess && cus > 0)
         ix->cus = static_cast<uint32_t>(cus);
@@ -394,7 +401,11 @@ int make_plan(bs_index ix, const bs_search_cfg* cfg, uint64_t nq, Plan& pl) {
     pl.CR = ix->degree <= 64 ? 1 : ix->degree <= 128 ? 2 : 4;
     bsd::L2Shape L = bsd::l2_shape(ix->dim);
     if (L.QR > 4) return fail(BS_EINVAL, "dim too large");
-    pl.PB = bsd::l2_passes_in_flight(L);
+    // 32 rows per batch for the hash-filter loop over rows of up to 128 dims: 1M x 128,
+    // degree 32: topk 256 4.58 -> 4.49 ms, topk 128 2.54 -> 2.39, topk 512 9.75 -> 8.66
+    // (with the larger visit filter below); the Bloom loop keeps 16 (its wavefronts per CU
+    // drop from 16 to 12 for nothing: bwarp1 5.46 -> 6.41 ms)
+    pl.PB = bsd::l2_passes_in_flight(L, (mode == BS_BASE || mode == BS_GROUP) && L.rpp >= 8u ? 32u : 16u);
 
     bsd::SearchParams& p = pl.p;
     std::memset(&p, 0, sizeof(p));
@@ -415,10 +426,13 @@ int make_plan(bs_index ix, const bs_search_cfg* cfg, uint64_t nq, Plan& pl) {
     // The hash filters (visit filter, RaBitQ expanded set) refuse keys as the reference's
     // table of 2^ceil(log2 capacity) slots does, but get more slots when the workgroup's LDS
     // allows it: probe runs at the same occupancy are shorter, the results are the same.
-    // The visit filter fills up between resets and gets twice the slots (config B: 5.0 ->
-    // 4.8 ms, topk 512: 20.1 -> 10.9 ms).  The RaBitQ expanded set ends with about one key
-    // per beam slot and gets 5T/3 slots within [cap, 2 cap] (topk 768: 2048 slots 14.0 ms,
-    // 1280 slots 12.8 ms: fewer slots, more wavefronts per CU).
+    // The visit filter fills up between resets: it gets at least twice the slots (config B:
+    // 5.0 -> 4.8 ms, topk 512: 20.1 -> 10.9 ms), and up to four times as many as the LDS
+    // left by the instance's register-limited residency holds (config B with 32-row L2
+    // batches: 2048 slots 4.54 ms, 2624 slots 4.43 ms; smaller tables that admit more
+    // wavefronts lost: 1344 slots at 20 wavefronts per CU 5.0 ms).  The RaBitQ expanded set
+    // ends with about one key per beam slot and gets 5T/3 slots within [cap, 2 cap] (topk
+    // 768: 2048 slots 14.0 ms, 1280 slots 12.8 ms: fewer slots, more wavefronts per CU).
     uint32_t scratch = 512u * pl.TR + 16u;  // the beam and the merge's dump slot
     if (mode == BS_RABITQ) {
         p.pdim = ix->pdim;
@@ -455,8 +469,18 @@ int make_plan(bs_index ix, const bs_search_cfg* cfg, uint64_t nq, Plan& pl) {
         p.filter_cap = 1u << b;
         const uint32_t base_slots = std::max(4u, p.filter_cap);
         if (mode != BS_RABITQ) {
-            // the visit filter fills up to cap between resets: twice the slots (a power of two)
             p.filter_slots = b < 11 ? base_slots * 2u : base_slots;
+            layout(0);
+            const uint32_t other = p.lds_wave;  // the slice without the filter
+            int wg = 0;                          // workgroups per CU the registers allow
+            if (bsd::launch_search_hash(p, pl.TR, pl.CR, pl.PB, dim3(1), dim3(64 * ny), 0, nullptr, &wg) ==
+                    hipSuccess &&
+                wg > 0) {
+                const uint32_t per_wave = static_cast<uint32_t>((ix->lds_cu / static_cast<size_t>(wg)) &
+                                                                ~static_cast<size_t>(LDS_GRANULE - 1)) / ny;
+                const uint32_t fit = per_wave > other ? (per_wave - other) / 4u / 64u * 64u : 0u;
+                if (fit > p.filter_slots) p.filter_slots = std::min(fit, 4u * base_slots);
+            }
         } else {
             // the expanded set holds about one key per beam slot: 5T/3 slots (a multiple of
             // 64), at least cap and at most 2 cap

@@ -335,7 +335,7 @@ __global__ void __launch_bounds__(64) dbg_filter_kernel(int bloom, uint32_t bits
     extern __shared__ __attribute__((aligned(16))) char smem[];
     const uint32_t lane = bsd::lane_id();
     if (!bloom) {
-        bsd::HashLds<true> h;
+        bsd::HashLds h;
         h.t = reinterpret_cast<uint32_t*>(smem);
         h.size = (1u << bits) >= 4u ? (1u << bits) : 4u;
         h.cap = 1u << bits;

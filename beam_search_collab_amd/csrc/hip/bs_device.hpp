@@ -474,36 +474,29 @@ __device__ __forceinline__ void sort_beam(uint64_t (&v)[TR]) {
 // from its home slot on; it sits in the first empty slot of its sequence at insertion and
 // slots never empty, so a lookup stops at the key (present) or an empty slot (absent).
 // Inserts go slot by slot (a compare-and-swap returns the slot's key); lookups read 4 slots
-// (16 B, one ds_read_b128) per step.  `occ` counts occupied slots (wave-uniform).
-//   POW2: 2^k slots, home = (k ^ (k >> log2 size)) & (size - 1) (the reference's hash);
-//   else: any multiple of 4 slots, home = (k * 0x9e3779b1) scaled to [0, size).
-template <bool POW2>
+// (16 B, one ds_read_b128) per step.  `occ` counts occupied slots (wave-uniform).  The
+// table has any multiple of 4 slots (sized to the LDS the wavefront's residency leaves), so
+// the home slot is a multiplicative hash scaled to [0, size) rather than the reference's
+// power-of-two mask; where a key sits never changes a result.
 struct HashLds {
     uint32_t* t;
-    uint32_t size;  // slots, a multiple of 4 (a power of two when POW2)
+    uint32_t size;  // slots, a multiple of 4
     uint32_t cap;   // keys accepted
     uint32_t occ;
 
     __device__ __forceinline__ uint32_t home(uint32_t k) const {
-        if constexpr (POW2) {
-            const uint32_t b = static_cast<uint32_t>(__builtin_ctz(size));
-            return (k ^ (k >> b)) & (size - 1u);
-        } else {
-            return static_cast<uint32_t>((static_cast<uint64_t>(k * 0x9E3779B1u) * size) >> 32);
-        }
+        return static_cast<uint32_t>((static_cast<uint64_t>(k * 0x9E3779B1u) * size) >> 32);
     }
-    __device__ __forceinline__ uint32_t next(uint32_t i) const {
-        if constexpr (POW2) return (i + 1) & (size - 1u);
-        else return i + 1 == size ? 0u : i + 1;
-    }
+    __device__ __forceinline__ uint32_t next(uint32_t i) const { return i + 1 == size ? 0u : i + 1; }
     __device__ __forceinline__ uint32_t add(uint32_t i, uint32_t d) const {  // d < size
-        if constexpr (POW2) return (i + d) & (size - 1u);
-        else return i + d >= size ? i + d - size : i + d;
+        return i + d >= size ? i + d - size : i + d;
     }
 
     __device__ __forceinline__ void clear() {
         const uint32_t lane = lane_id();
-        for (uint32_t i = lane; i < size; i += 64) t[i] = INVALID;
+        uint4* t4 = reinterpret_cast<uint4*>(t);
+        const uint4 e = make_uint4(INVALID, INVALID, INVALID, INVALID);
+        for (uint32_t i = lane; i < (size >> 2); i += 64) t4[i] = e;
         occ = 0;
         wave_sync();
     }
@@ -710,10 +703,12 @@ struct L2Shape {
 // (1 <= G <= 64), so each lane holds QR = ceil(chunks/G) <= 4 chunks (for dim <= 1024) and a
 // 64-lane pass covers 64/G rows.  Four chunks per lane keep the butterfly short (log2 G
 // steps per pass) and put 64/G rows of loads in flight per pass.
-// Passes in flight for l2_rows: about 16 rows per batch, 2..8 passes (at most 128 VGPRs
-// of loads; a row of dim > 256 spans 32 or 64 lanes, so one pass holds only 1-2 rows).
-__host__ __device__ inline int l2_passes_in_flight(const L2Shape& L) {
-    const uint32_t pb = 16u / L.rpp;
+// Passes in flight for l2_rows: about `rows` rows per batch, 2..8 passes (at most 128
+// VGPRs of loads; a row of dim > 256 spans 32 or 64 lanes, so one pass holds only 1-2
+// rows).  The search asks for 16 rows, or 32 for hash-filter searches over rows of up to
+// 128 dims (a degree-32 neighbour list in one HBM round trip).
+__host__ __device__ inline int l2_passes_in_flight(const L2Shape& L, uint32_t rows = 16) {
+    const uint32_t pb = rows / L.rpp;
     return pb <= 2u ? 2 : pb >= 8u ? 8 : static_cast<int>(pb);
 }
 

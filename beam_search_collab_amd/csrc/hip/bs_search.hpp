@@ -43,9 +43,8 @@ struct SearchParams {
 
 // Register budget per instance, matched to what the LDS slice allows anyway: RaBitQ beams
 // up to 256 (about 7 KB of LDS per wavefront) are compiled for 5 wavefronts per SIMD (at most
-// 96 VGPRs); the base loop with beams up to 256 and rows of at most 128 dims (PB = 2) holds
-// a 2048-slot filter (about 11 KB, at most 15 wavefronts per CU), so it gets 4 (128 VGPRs,
-// no spills).
+// 96 VGPRs); the loops with beams up to 256 and two passes of rows in flight (Bloom over rows
+// of up to 128 dims, hash over rows of up to 64) get 4 (128 VGPRs, no spills).
 template <int TR, int CR, int MODE, int PB>
 constexpr int min_waves_per_simd() {
     return (CR != 1 || TR > 4) ? 1 : MODE == MODE_RABITQ ? 5 : PB == 2 ? 4 : 1;
@@ -105,7 +104,7 @@ search_kernel(const SearchParams p) {
             return;
         }
 
-        HashLds<true> hf;
+        HashLds hf;
         BloomLds bf;
         if constexpr (MODE == MODE_HASH) {
             hf.t = reinterpret_cast<uint32_t*>(my + p.off_filter);
@@ -275,7 +274,7 @@ search_kernel(const SearchParams p) {
         }
     } else {
         // ---------------------------------------------------------------- rabitq
-        HashLds<false> hf;
+        HashLds hf;
         hf.t = reinterpret_cast<uint32_t*>(my + p.off_filter);
         hf.size = p.filter_slots;
         hf.cap = p.filter_cap;
