@@ -278,17 +278,19 @@ def cpu_baseline(files, nq_total, run, args):
 def kernel_name(mode, topk, degree, dim):
     """symbol of the search-kernel instance a launch uses (beam registers TR = topk/64 rounded
     up to 1, 2, 4, 8, 16, or 12 for rabitq beams of 513..768,
-    candidate registers CR = degree/64, 4 float4 chunks per lane, filter/mode id, row
-    passes in flight PB from the L2 row shape)"""
+    candidate registers CR = degree/64 rounded up to 1, 2, 4, 4 float4 chunks per lane, filter/mode id, row
+    passes in flight PB from the L2 row shape and the rows per batch)"""
     m = {"base": 0, "warp": 0, "bwarp": 1, "rabitq": 2}[mode.rstrip("0123456789")]
     tr = 1 if topk <= 64 else 2 if topk <= 128 else 4 if topk <= 256 else 8 if topk <= 512 else \
         12 if (topk <= 768 and m == 2) else 16
-    cr = 1 if degree <= 64 else 2
+    cr = 1 if degree <= 64 else 2 if degree <= 128 else 4
     p = 1
     while p < (dim + 3) // 4:
         p *= 2
     g = min(max(p // 4, 1), 64)
-    pb = min(max(16 // (64 // g), 2), 8)
+    # rows per batch: 32 for the hash-filter loop over rows of up to 128 dims, 16 otherwise
+    rows = 32 if (m == 0 and 64 // g >= 8) else 16
+    pb = min(max(rows // (64 // g), 2), 8)
     if m == 2 and dim > 128:
         m = 3  # rabitq with wide codes (pdim > 128)
     return f"bsd::search_kernel<{tr}, {cr}, 4, {m}, {pb}>"
@@ -360,7 +362,8 @@ def measure_traffic(args, cache, searches, keep=""):
         ds = [d for d, (k, _) in rd.items() if kn in k]
         dw = [d for d, (k, _) in wr.items() if kn in k]
         if len(ds) < 3 or len(dw) < 3:
-            return f"{kn}: {len(ds)} / {len(dw)} dispatches in the counter passes"
+            seen = sorted({k for _, (k, _) in rd.items() if "search_kernel" in k})
+            return f"{kn}: {len(ds)} / {len(dw)} dispatches in the counter passes (search kernels seen: {seen})"
         ds, dw = ds[-2:], dw[-2:]  # the two counted launches (after the warm-up)
         rb = sum(read_bytes(rd[d][1]) for d in ds) / len(ds)
         wb = sum(wr[d][1]["WRITE_SIZE"] * 1024.0 for d in dw) / len(dw)
