@@ -457,6 +457,10 @@ int make_plan(bs_index ix, const bs_search_cfg* cfg, uint64_t nq, Plan& pl) {
         if (mode == BS_RABITQ) p.off_planes = planes_rel + p.off_scratch;
         p.off_coop = p.off_cand + 64u * pl.CR * 8u + 8u * std::max(pl.TR, 8);  // after the merge's slot bitmap
         p.lds_wave = al(p.off_coop + 4u);
+        if (mode == BS_RABITQ && pl.TR >= 8) {  // the deferred merge's pending list
+            p.off_pend = p.lds_wave;
+            p.lds_wave += 64u * 8u;
+        }
     };
     if (mode == BS_GROUP_BLOOM) {
         uint32_t b = log2_ceil(cap);

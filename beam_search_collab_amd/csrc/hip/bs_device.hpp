@@ -324,6 +324,60 @@ __device__ __forceinline__ void beam_merge(uint64_t (&beam)[TR], const uint64_t 
 // register where it found its key.
 // next_key (optional): the unexpanded key that follows the picked one in the beam
 // (EMPTY_KEY if none), for a prediction of the following pick.
+// beam_pick in two steps, for the deferred merge's pick (pending_pick): the beam's smallest
+// unexpanded key (EMPTY_KEY if none), not marked; `at` = its slot 64 r + l, st.first
+// advances to its register.
+template <int TR>
+__device__ __forceinline__ uint64_t beam_peek(const uint64_t (&beam)[TR], BeamState& st, uint32_t& at,
+                                              uint64_t& row_mask) {
+    uint32_t pr = st.first;
+    uint64_t row, mp;
+    for (;;) {
+        if (pr >= static_cast<uint32_t>(TR)) {
+            st.first = pr;
+            at = 64u * TR;
+            row_mask = 0;
+            return EMPTY_KEY;
+        }
+        row = beam_reg<TR>(beam, pr);
+        mp = ballot((static_cast<uint32_t>(row) & 1u) == 0u);
+        if (mp != 0) break;
+        ++pr;
+    }
+    st.first = pr;
+    const uint32_t pl = static_cast<uint32_t>(__builtin_ctzll(mp));
+    at = 64u * pr + pl;
+    row_mask = mp;
+    return readlane64(row, pl);
+}
+
+// Mark the beam key kp found by beam_peek at slot `at`.  RUN: of a run of identical keys
+// the last one is marked, which keeps the beam sorted.
+template <int TR, bool RUN>
+__device__ __forceinline__ void beam_mark(uint64_t (&beam)[TR], BeamState& st, uint32_t at, uint64_t kp) {
+    const uint32_t pr = at >> 6, pl = at & 63u;
+    uint32_t qr = pr, ql = pl;
+    if constexpr (RUN) {
+        // identical keys are rare: look at the next element first, scan only if it repeats
+        uint64_t nxt = EMPTY_KEY;
+        if (pl < 63u) nxt = readlane64(beam_reg<TR>(beam, pr), pl + 1u);
+        else if (pr + 1u < static_cast<uint32_t>(TR)) nxt = readlane64(beam_reg<TR>(beam, pr + 1u), 0u);
+        if (nxt == kp) {
+#pragma unroll
+            for (int r = 0; r < TR; ++r) {
+                const uint64_t mm = ballot(beam[r] == kp);
+                if (static_cast<uint32_t>(r) >= pr && mm != 0) {
+                    qr = static_cast<uint32_t>(r);
+                    ql = 63u - static_cast<uint32_t>(__builtin_clzll(mm));
+                }
+            }
+        }
+    }
+    // set the mark (key LSB) of element (qr, ql)
+    beam[qr] |= bsw::lane_in(1ull << ql) ? 1ull : 0ull;
+    if constexpr (merge_split<TR, 1>()) st.last |= bsw::lane_in(ql == 63u ? 1ull << qr : 0ull) ? 1ull : 0ull;
+}
+
 template <int TR, bool RUN>
 __device__ __forceinline__ uint32_t beam_pick(uint64_t (&beam)[TR], BeamState& st, uint64_t* next_key = nullptr) {
     // the first register holding an unexpanded key, its first such lane
@@ -380,6 +434,159 @@ __device__ __forceinline__ uint32_t beam_pick(uint64_t (&beam)[TR], BeamState& s
     beam[qr] |= bsw::lane_in(1ull << ql) ? 1ull : 0ull;
     if constexpr (merge_split<TR, 1>()) st.last |= bsw::lane_in(ql == 63u ? 1ull << qr : 0ull) ? 1ull : 0ull;
     return key_id(kp);
+}
+
+// exact 64-bit minimum of v over the wave (every lane active): the upper words' minimum by
+// a butterfly in rows of 16 and the rows' results, then, when more than one lane holds that
+// upper word, the lower words' minimum among them
+__device__ __forceinline__ uint64_t wave_min64(uint64_t v) {
+    const uint32_t vh = static_cast<uint32_t>(v >> 32);
+    uint32_t h = vh;
+    h = min(h, bsw::xor_lane<1>(h));
+    h = min(h, bsw::xor_lane<2>(h));
+    h = min(h, bsw::xor_lane<4>(h));
+    h = min(h, bsw::xor_lane<8>(h));
+    const uint32_t m = min(min(readlane(h, 0), readlane(h, 16)), min(readlane(h, 32), readlane(h, 48)));
+    const uint64_t at = ballot(vh == m);
+    const uint32_t l0 = static_cast<uint32_t>(__builtin_ctzll(at));
+    if ((at & (at - 1u)) == 0) return (static_cast<uint64_t>(m) << 32) | readlane(static_cast<uint32_t>(v), l0);
+    uint32_t lo = bsw::lane_in(at) ? static_cast<uint32_t>(v) : 0xFFFFFFFFu;
+    lo = min(lo, bsw::xor_lane<1>(lo));
+    lo = min(lo, bsw::xor_lane<2>(lo));
+    lo = min(lo, bsw::xor_lane<4>(lo));
+    lo = min(lo, bsw::xor_lane<8>(lo));
+    const uint32_t ml = min(min(readlane(lo, 0), readlane(lo, 16)), min(readlane(lo, 32), readlane(lo, 48)));
+    return (static_cast<uint64_t>(m) << 32) | ml;
+}
+
+// ---------------------------------------------------------------------------
+// Deferred merge.  The beam must hold the T smallest keys merged so far, and a key
+// evicted once never returns (the T-th key only falls).  So candidates need not enter
+// the beam at once: those below the beam's last key are appended to a pending list of up
+// to 64 keys in LDS, which is merged into the beam (beam_merge) when it would overflow
+// and whenever the beam itself is needed (filter re-fill, rerank, results).  The T
+// smallest of (beam U list) are exactly the T smallest keys merged so far (a key the beam
+// evicted or the list refused has at least T smaller keys).  The pick takes the smallest
+// unmarked key u of beam and list: u is among the T smallest iff fewer than T keys of the
+// union are smaller, and those are all marked, so the count is needed only once T picks
+// have been made.  Identical keys are indistinguishable: which copy carries the mark does
+// not change the multiset of (key, mark) pairs, so every pick, merge and result is the one
+// of an immediate merge.
+// ---------------------------------------------------------------------------
+struct PendingList {
+    uint64_t* k;   // 64 keys in the wave's LDS
+    uint32_t n;    // keys held
+};
+
+__device__ __forceinline__ uint64_t pending_reg(const PendingList& pd) {
+    const uint32_t lane = lane_id();
+    const uint64_t v = pd.k[lane];
+    return lane < pd.n ? v : EMPTY_KEY;
+}
+
+template <int TR>
+__device__ __forceinline__ void pending_flush(uint64_t (&beam)[TR], PendingList& pd, uint32_t T, uint64_t* scratch,
+                                              uint64_t* aux, BeamState& st) {
+    if (pd.n == 0) return;
+    const uint64_t ck[1] = {pending_reg(pd)};
+    const uint64_t cm[1] = {pd.n >= 64u ? ~0ull : (1ull << pd.n) - 1ull};
+    beam_merge<TR, 1>(beam, ck, cm, T, scratch, aux, st);
+    pd.n = 0;
+}
+
+// candidates ck (lanes cm) below the beam's last key into the list; a full list is merged
+// first, and candidates that do not fit even then are merged directly
+template <int TR, int CR>
+__device__ __forceinline__ void pending_add(uint64_t (&beam)[TR], const uint64_t (&ck)[CR], const uint64_t (&cm)[CR],
+                                            PendingList& pd, uint32_t T, uint64_t* scratch, uint64_t* aux,
+                                            BeamState& st) {
+    uint64_t thr = readlane64(beam_reg<TR>(beam, (T - 1) >> 6), (T - 1) & 63u);
+    uint64_t ok[CR];
+    uint32_t n = 0;
+#pragma unroll
+    for (int rc = 0; rc < CR; ++rc) {
+        ok[rc] = cm[rc] & ballot(ck[rc] < thr);
+        n += static_cast<uint32_t>(__builtin_popcountll(ok[rc]));
+    }
+    if (n == 0) return;
+    if (pd.n + n > 64u) {
+        pending_flush<TR>(beam, pd, T, scratch, aux, st);
+        thr = readlane64(beam_reg<TR>(beam, (T - 1) >> 6), (T - 1) & 63u);
+        n = 0;
+#pragma unroll
+        for (int rc = 0; rc < CR; ++rc) {
+            ok[rc] &= ballot(ck[rc] < thr);
+            n += static_cast<uint32_t>(__builtin_popcountll(ok[rc]));
+        }
+        if (n == 0) return;
+        if (n > 64u) {
+            beam_merge<TR, CR>(beam, ck, ok, T, scratch, aux, st);
+            return;
+        }
+    }
+    uint32_t at = pd.n;
+#pragma unroll
+    for (int rc = 0; rc < CR; ++rc) {
+        if (bsw::lane_in(ok[rc])) pd.k[at + bsw::lanes_below(ok[rc])] = ck[rc];
+        at += static_cast<uint32_t>(__builtin_popcountll(ok[rc]));
+    }
+    pd.n = at;
+    wave_sync();
+}
+
+// pick over beam and list (the beam_pick of an immediately merged beam); picks = marks
+// made so far, counted here.  With RUN, a key held unmarked more than once is picked from
+// the merged beam: the immediate merge may have evicted some of its copies, and which
+// copies are left decides which one carries the mark, so the list is merged first.
+template <int TR, bool RUN>
+__device__ __forceinline__ uint32_t pending_pick(uint64_t (&beam)[TR], BeamState& st, PendingList& pd, uint32_t T,
+                                                 uint64_t* scratch, uint64_t* aux, uint32_t& picks) {
+    const uint32_t lane = lane_id();
+    uint32_t at;
+    uint64_t mp;
+    const uint64_t ub = beam_peek<TR>(beam, st, at, mp);
+    // the list's smallest unmarked key
+    const uint64_t v = pending_reg(pd);
+    const uint64_t pmin = pd.n > 0 ? wave_min64((v & 1ull) ? EMPTY_KEY : v) : EMPTY_KEY;
+    const bool from_list = pmin <= ub && pmin != EMPTY_KEY;
+    const uint64_t u = from_list ? pmin : ub;
+    if (u == EMPTY_KEY) return INVALID;
+    if constexpr (RUN) {
+        if (pd.n > 0) {
+            bool dup;
+            if (from_list) {
+                dup = ub == u || __builtin_popcountll(ballot(v == u)) >= 2;
+            } else {
+                // the beam's unmarked copies of u follow it
+                const uint32_t nx = at + 1u;
+                const uint64_t kn = nx < 64u * TR ? readlane64(beam_reg<TR>(beam, nx >> 6), nx & 63u) : EMPTY_KEY;
+                dup = kn == u;
+            }
+            if (dup) {
+                pending_flush<TR>(beam, pd, T, scratch, aux, st);
+                const uint32_t id = beam_pick<TR, true>(beam, st);
+                picks += id != INVALID ? 1u : 0u;
+                return id;
+            }
+        }
+    }
+    if (picks >= T) {
+        // u must be among the T smallest of beam U list
+        uint32_t below = 0;
+#pragma unroll
+        for (int r = 0; r < TR; ++r) below += static_cast<uint32_t>(__builtin_popcountll(ballot(beam[r] < u)));
+        below += static_cast<uint32_t>(__builtin_popcountll(ballot(v < u)));
+        if (below >= T) return INVALID;
+    }
+    ++picks;
+    if (from_list) {
+        const uint32_t l = static_cast<uint32_t>(__builtin_ctzll(ballot(v == u)));
+        if (lane == l) pd.k[l] = v | 1ull;
+        wave_sync();
+    } else {
+        beam_mark<TR, RUN>(beam, st, at, ub);
+    }
+    return key_id(u);
 }
 
 // The smallest key held by the lanes of k[0..CR) (EMPTY_KEY if none), for the prediction

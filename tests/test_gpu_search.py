@@ -279,6 +279,22 @@ def test_degree_above_128_four_candidate_registers(gpu, degree, dim, mode):
         assert_same(*run_both(ds, mode, 10, topk), f"{mode} R={degree} d={dim} topk={topk}")
 
 
+@pytest.mark.parametrize("dim,degree,kind,topk,cap", [(64, 100, "normalized", 768, 1024),
+                                                      (64, 100, "normalized", 512, 64),
+                                                      (32, 16, "mixture", 600, 1024),
+                                                      (128, 32, "mixture", 1024, 256),
+                                                      (100, 64, "normalized", 768, 32),
+                                                      (25, 24, "normalized", 512, 1024)])
+def test_rabitq_deferred_merge(gpu, dim, degree, kind, topk, cap):
+    """rabitq beams of more than 256 keys defer the merge: candidates wait in a list of up to
+    64 keys, merged when it would overflow, when the pick meets a key held unmarked twice and
+    before the rerank.  Ids, distances and every counter must equal the oracle's immediate
+    merge, with duplicate (estimate, id) keys (normalized data), lists that overflow with two
+    candidate registers, and expanded sets that fill (capacities 32-256)"""
+    ds = dataset(2500, dim, degree, 40, kind)
+    assert_same(*run_both(ds, "rabitq", 10, topk, cap=cap), f"rabitq d={dim} R={degree} topk={topk} cap={cap}")
+
+
 @pytest.mark.parametrize("degree", [48, 64, 100])
 @pytest.mark.parametrize("ny", [1, 4])
 def test_bloom_rounds_small_filters(gpu, degree, ny):
