@@ -323,8 +323,6 @@ search_kernel(const SearchParams p) {
             const uint32_t parent = DEFER ? pending_pick<TR, true>(beam, st, pd, T, scratch, merge_aux, picks)
                                           : beam_pick<TR, true>(beam, st);
             if (parent == INVALID) break;
-            if (!hf.insert1(parent)) continue;  // already expanded (gpu_search_rabitq.cuh:249-252)
-            ++n_exp;
             const uint32_t* rec = p.recs + static_cast<uint64_t>(parent) * rstride;
             const float* fac = reinterpret_cast<const float*>(rec + p.rec_fac);
             const uint32_t* codes = rec + p.rec_codes;
@@ -361,6 +359,11 @@ search_kernel(const SearchParams p) {
                     cw[t] = load_quad(codes, nb, p.R, qi, S);
                 }
             }
+            // The expanded set is probed while the record is in flight: the loads of a node
+            // already expanded (gpu_search_rabitq.cuh:249-252; 7.5% of the picks at config C)
+            // are wasted, the probe's LDS latency of every other pick is hidden.
+            if (!hf.insert1(parent)) continue;
+            ++n_exp;
 
             // exact distance of the parent
             float pe[1];
