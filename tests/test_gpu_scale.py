@@ -1,8 +1,11 @@
-"""Parity at the benchmark's own size: config B (1M x 128 fp32 64-centre mixture, 10k queries,
-degree-32 Vamana, base mode, topk 256, K 100) and config C (the same index with the RaBitQ
-codebook, topk 768, K 10).  The GPU searches all 10k queries in one launch (query scheduling,
-every wavefront slot busy, the launch's tail); the oracle restates the search for 48 of them,
-spread over the set, and ids, distances and the per-query counters must be identical."""
+"""Parity at the benchmarks' own sizes: config B (1M x 128 fp32 64-centre mixture, 10k queries,
+degree-32 Vamana, base mode, topk 256, K 100), config C (the same index with the RaBitQ
+codebook, topk 768, K 10), config D (1.2M x 100 normalised N(0,1), degree 64, warp1 and bwarp2,
+topk 128, K 10) and config E (1M x 960 256-centre mixture, 1k queries, base and rabitq with
+960-bit codes, topk 256, K 100).  The GPU searches every query of the config in one launch
+(query scheduling, every wavefront slot busy, the launch's tail); the oracle restates the
+search for a sample spread over the set, and ids, distances and the per-query counters must
+be identical."""
 import numpy as np
 import pytest
 
@@ -27,6 +30,7 @@ def config_b(gpu):
 
 def run_device(g, queries, K, mode, cfg):
     import torch
+    NQ = queries.shape[0]
     dev = torch.device("cuda:0")
     q_t = torch.from_numpy(queries).to(dev)
     res = torch.empty((NQ, K), dtype=torch.int32, device=dev)
@@ -37,13 +41,13 @@ def run_device(g, queries, K, mode, cfg):
     return (res.cpu().numpy().astype(np.uint32), dist.cpu().numpy(), pq.cpu().numpy().astype(np.uint64))
 
 
-def compare(ids, d, pq, oids, od, ost, what):
-    bad = np.nonzero((ids[SAMPLE] != oids).any(1))[0]
-    assert len(bad) == 0, f"{what}: queries {SAMPLE[bad][:5]} differ"
-    assert d[SAMPLE].tobytes() == od.tobytes(), what
+def compare(ids, d, pq, oids, od, ost, what, sample=SAMPLE):
+    bad = np.nonzero((ids[sample] != oids).any(1))[0]
+    assert len(bad) == 0, f"{what}: queries {sample[bad][:5]} differ"
+    assert d[sample].tobytes() == od.tobytes(), what
     # iterations, expansions, distance evaluations (and estimates for rabitq) per query
     cols = [0, 1, 2, 3] if what.startswith("rabitq") else [0, 1, 2]
-    assert np.array_equal(pq[SAMPLE][:, cols], ost[:, cols]), what
+    assert np.array_equal(pq[sample][:, cols], ost[:, cols]), what
 
 
 def test_config_b_base_full_launch_matches_oracle(config_b):
@@ -66,3 +70,40 @@ def test_config_c_rabitq_full_launch_matches_oracle(config_b):
     oi = po.OracleIndex(base, edges, codes, factors, signs)
     oids, od, ost = oi.search(queries[SAMPLE], 10, po.RABITQ_GPU, 768, erq, 1024, 1024, 0, po.L2_WAVE)
     compare(ids, d, pq, oids, od, ost, "rabitq topk 768")
+
+
+@pytest.fixture(scope="module")
+def config_d(gpu):
+    base = host.gen_normalized(1_200_000, 100, 202)
+    queries = host.gen_normalized(NQ, 100, 303)
+    edges = search.build_vamana_device(base, 64, 128, 2.0, 1234)
+    return base, queries, edges, search.GPUGraph(base, edges)
+
+
+@pytest.mark.parametrize("mode,omode", [("warp1", po.BASE_HASH), ("bwarp2", po.BASE_BLOOM)])
+def test_config_d_full_launch_matches_oracle(config_d, mode, omode):
+    base, queries, edges, g = config_d
+    entry = g.entry_point()
+    ids, d, pq = run_device(g, queries, 10, mode, GPUBaseSearchCfg(128, 1024, entry, 1024, 16))
+    oi = po.OracleIndex(base, edges)
+    oids, od, ost = oi.search(queries[SAMPLE], 10, omode, 128, entry, 1024, 1024, 16, po.L2_WAVE)
+    compare(ids, d, pq, oids, od, ost, f"{mode} topk 128")
+
+
+def test_config_e_full_launch_matches_oracle(gpu):
+    base = host.gen_mixture(1_000_000, 960, 256, 0.0, 1.0, 0.05, 0.0, 101, 202)
+    queries = host.gen_mixture(1000, 960, 256, 0.0, 1.0, 0.05, 0.0, 101, 303)
+    edges = search.build_vamana_device(base, R, 128, 2.0, 1234)
+    g = search.GPUGraph(base, edges)
+    sample = np.linspace(0, 999, 24).astype(np.int64)
+    entry = g.entry_point()
+    ids, d, pq = run_device(g, queries, 100, "base", GPUBaseSearchCfg(256, 1024, entry, 1024, 16))
+    oi = po.OracleIndex(base, edges)
+    oids, od, ost = oi.search(queries[sample], 100, po.BASE_HASH, 256, entry, 1024, 1024, 16, po.L2_WAVE)
+    compare(ids, d, pq, oids, od, ost, "base d960 topk 256", sample)
+    erq, codes, factors, signs = g.build_rabitq(12345)
+    g.attach_rabitq(codes, factors, signs)
+    ids, d, pq = run_device(g, queries, 100, "rabitq", GPURabitqSearchCfg(256, 1024, erq, 1024))
+    oi = po.OracleIndex(base, edges, codes, factors, signs)
+    oids, od, ost = oi.search(queries[sample], 100, po.RABITQ_GPU, 256, erq, 1024, 1024, 0, po.L2_WAVE)
+    compare(ids, d, pq, oids, od, ost, "rabitq d960 topk 256", sample)
