@@ -3,8 +3,8 @@
 // Exchanges used by the reductions and the bitonic sorter:
 //   xor 1, 2      DPP quad_perm                      (VALU, no LDS traffic)
 //   xor 4, 8      two DPP mirrors (row_half_mirror/row_mirror composed with quad reverse)
-//   xor 16        ds_swizzle bit-mask mode (within 32-lane halves)
-//   xor 32        ds_bpermute
+//   xor 16        v_permlane16_swap + a select       (VALU)
+//   xor 32        v_permlane32_swap + a select       (VALU)
 //   shift by one  ds_bpermute
 #pragma once
 #include <hip/hip_runtime.h>
@@ -75,11 +75,16 @@ __device__ __forceinline__ uint32_t xor_lane(uint32_t v) {
     } else if constexpr (S == 8) {
         return dpp<DPP_HALF_MIRROR>(dpp<DPP_MIRROR>(v));   // (i ^ 15) ^ 7 = i ^ 8
     } else if constexpr (S == 16) {
-        return static_cast<uint32_t>(__builtin_amdgcn_ds_swizzle(static_cast<int>(v), 0x401F));
+        // v_permlane16_swap (gfx950): of swap(v, v), result 0 holds rows 0,0,2,2 and result 1
+        // rows 1,1,3,3 of v (rows of 16 lanes), so rows 0 and 2 take result 1
+        const auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+        return lane_in(0x0000FFFF0000FFFFull) ? r[1] : r[0];
     } else {
         static_assert(S == 32, "xor distance must be a power of two below 64");
-        return static_cast<uint32_t>(
-            __builtin_amdgcn_ds_bpermute(static_cast<int>((lane_id() ^ 32u) << 2), static_cast<int>(v)));
+        // v_permlane32_swap (gfx950): of swap(v, v), result 0 holds the lower half of v twice
+        // and result 1 the upper half twice, so lanes 0-31 take result 1
+        const auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+        return lane_in(0x00000000FFFFFFFFull) ? r[1] : r[0];
     }
 }
 
