@@ -469,9 +469,11 @@ __device__ __forceinline__ uint64_t wave_min64(uint64_t v) {
 // evicted or the list refused has at least T smaller keys).  The pick takes the smallest
 // unmarked key u of beam and list: u is among the T smallest iff fewer than T keys of the
 // union are smaller, and those are all marked, so the count is needed only once T picks
-// have been made.  Identical keys are indistinguishable: which copy carries the mark does
-// not change the multiset of (key, mark) pairs, so every pick, merge and result is the one
-// of an immediate merge.
+// have been made.  Identical keys are indistinguishable, so which copy of a key carries a
+// mark does not matter -- except when a key is held unmarked more than once (RaBitQ): the
+// immediate merge may have evicted some of those copies, so such a pick merges the list
+// first (pending_pick).  With that rule every pick, merge and result is the one of an
+// immediate merge (checked against the oracle, which merges at once).
 // ---------------------------------------------------------------------------
 struct PendingList {
     uint64_t* k;   // 64 keys in the wave's LDS
