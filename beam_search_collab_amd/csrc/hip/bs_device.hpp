@@ -476,24 +476,20 @@ __device__ __forceinline__ uint64_t wave_min64(uint64_t v) {
 // immediate merge (checked against the oracle, which merges at once).
 // ---------------------------------------------------------------------------
 struct PendingList {
-    uint64_t* k;   // 64 keys in the wave's LDS
+    uint64_t* k;   // 64 key slots in the wave's LDS, the staging area of appends
     uint32_t n;    // keys held
+    uint64_t v;    // the list itself: key `lane` in lane `lane` (< n), EMPTY_KEY above
 };
-
-__device__ __forceinline__ uint64_t pending_reg(const PendingList& pd) {
-    const uint32_t lane = lane_id();
-    const uint64_t v = pd.k[lane];
-    return lane < pd.n ? v : EMPTY_KEY;
-}
 
 template <int TR>
 __device__ __forceinline__ void pending_flush(uint64_t (&beam)[TR], PendingList& pd, uint32_t T, uint64_t* scratch,
                                               uint64_t* aux, BeamState& st) {
     if (pd.n == 0) return;
-    const uint64_t ck[1] = {pending_reg(pd)};
+    const uint64_t ck[1] = {pd.v};
     const uint64_t cm[1] = {pd.n >= 64u ? ~0ull : (1ull << pd.n) - 1ull};
     beam_merge<TR, 1>(beam, ck, cm, T, scratch, aux, st);
     pd.n = 0;
+    pd.v = EMPTY_KEY;
 }
 
 // candidates ck (lanes cm) below the beam's last key into the list; a full list is merged
@@ -526,7 +522,10 @@ __device__ __forceinline__ void pending_add(uint64_t (&beam)[TR], const uint64_t
             return;
         }
     }
-    uint32_t at = pd.n;
+    // the new keys are compacted through the LDS slots above the list's end; the slots
+    // below it are stale (marks are set in the register copy only) and not read
+    const uint32_t n0 = pd.n;
+    uint32_t at = n0;
 #pragma unroll
     for (int rc = 0; rc < CR; ++rc) {
         if (bsw::lane_in(ok[rc])) pd.k[at + bsw::lanes_below(ok[rc])] = ck[rc];
@@ -534,6 +533,9 @@ __device__ __forceinline__ void pending_add(uint64_t (&beam)[TR], const uint64_t
     }
     pd.n = at;
     wave_sync();
+    const uint32_t lane = lane_id();
+    const uint64_t r = pd.k[lane];
+    pd.v = lane < n0 ? pd.v : (lane < at ? r : EMPTY_KEY);
 }
 
 // pick over beam and list (the beam_pick of an immediately merged beam); picks = marks
@@ -544,26 +546,25 @@ template <int TR, bool RUN>
 __device__ __forceinline__ uint32_t pending_pick(uint64_t (&beam)[TR], BeamState& st, PendingList& pd, uint32_t T,
                                                  uint64_t* scratch, uint64_t* aux, uint32_t& picks) {
     const uint32_t lane = lane_id();
+    const uint64_t v = pd.v;
     uint32_t at;
     uint64_t mp;
     const uint64_t ub = beam_peek<TR>(beam, st, at, mp);
     // the list's smallest unmarked key
-    const uint64_t v = pending_reg(pd);
     const uint64_t pmin = pd.n > 0 ? wave_min64((v & 1ull) ? EMPTY_KEY : v) : EMPTY_KEY;
     const bool from_list = pmin <= ub && pmin != EMPTY_KEY;
     const uint64_t u = from_list ? pmin : ub;
     if (u == EMPTY_KEY) return INVALID;
+    // a pick from the beam: the key after it, read once for the duplicate check and the mark
+    // (the beam's unmarked copies of u follow it)
+    uint64_t kn = EMPTY_KEY;
+    if (RUN && !from_list) {
+        const uint32_t nx = at + 1u;
+        if (nx < 64u * TR) kn = readlane64(beam_reg<TR>(beam, nx >> 6), nx & 63u);
+    }
     if constexpr (RUN) {
         if (pd.n > 0) {
-            bool dup;
-            if (from_list) {
-                dup = ub == u || __builtin_popcountll(ballot(v == u)) >= 2;
-            } else {
-                // the beam's unmarked copies of u follow it
-                const uint32_t nx = at + 1u;
-                const uint64_t kn = nx < 64u * TR ? readlane64(beam_reg<TR>(beam, nx >> 6), nx & 63u) : EMPTY_KEY;
-                dup = kn == u;
-            }
+            const bool dup = from_list ? (ub == u || __builtin_popcountll(ballot(v == u)) >= 2) : kn == u;
             if (dup) {
                 pending_flush<TR>(beam, pd, T, scratch, aux, st);
                 const uint32_t id = beam_pick<TR, true>(beam, st);
@@ -583,10 +584,12 @@ __device__ __forceinline__ uint32_t pending_pick(uint64_t (&beam)[TR], BeamState
     ++picks;
     if (from_list) {
         const uint32_t l = static_cast<uint32_t>(__builtin_ctzll(ballot(v == u)));
-        if (lane == l) pd.k[l] = v | 1ull;
-        wave_sync();
+        pd.v = v | (lane == l ? 1ull : 0ull);
+    } else if (RUN && kn == u) {
+        beam_mark<TR, true>(beam, st, at, ub);
     } else {
-        beam_mark<TR, RUN>(beam, st, at, ub);
+        // u is the last of its run: mark it in place
+        beam_mark<TR, false>(beam, st, at, ub);
     }
     return key_id(u);
 }

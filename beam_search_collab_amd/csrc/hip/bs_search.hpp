@@ -315,7 +315,7 @@ search_kernel(const SearchParams p) {
         // keys (pending_add); 1M x 128, 10k queries: topk 768 8.87 -> 8.11 ms, 512 6.11 ->
         // 5.95, while smaller beams lose (256 2.67 -> 2.73, 128 1.47 -> 1.61)
         constexpr bool DEFER = TR >= 8;
-        PendingList pd = {DEFER ? reinterpret_cast<uint64_t*>(my + p.off_pend) : nullptr, 0u};  // LDS only when DEFER
+        PendingList pd = {DEFER ? reinterpret_cast<uint64_t*>(my + p.off_pend) : nullptr, 0u, EMPTY_KEY};  // LDS only when DEFER
         uint32_t picks = 0;
 
         for (int32_t iter = 0; iter < p.max_it; ++iter) {
