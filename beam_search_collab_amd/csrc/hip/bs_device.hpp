@@ -463,7 +463,7 @@ __device__ __forceinline__ uint64_t wave_min64(uint64_t v) {
 // Deferred merge.  The beam must hold the T smallest keys merged so far, and a key
 // evicted once never returns (the T-th key only falls).  So candidates need not enter
 // the beam at once: those below the beam's last key are appended to a pending list of up
-// to 64 keys in LDS, which is merged into the beam (beam_merge) when it would overflow
+// to 64 keys (one per lane), which is merged into the beam (beam_merge) when it would overflow
 // and whenever the beam itself is needed (filter re-fill, rerank, results).  The T
 // smallest of (beam U list) are exactly the T smallest keys merged so far (a key the beam
 // evicted or the list refused has at least T smaller keys).  The pick takes the smallest
