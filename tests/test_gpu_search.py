@@ -295,6 +295,20 @@ def test_rabitq_deferred_merge(gpu, dim, degree, kind, topk, cap):
     assert_same(*run_both(ds, "rabitq", 10, topk, cap=cap), f"rabitq d={dim} R={degree} topk={topk} cap={cap}")
 
 
+@pytest.mark.parametrize("topk", [513, 768, 1024])
+def test_rabitq_deferred_merge_iteration_limits(gpu, topk):
+    """the deferred merge when the loop ends by max_iterations with keys still in the list
+    (merged before the rerank), with K beyond one register, and on a graph smaller than the
+    beam (the beam never fills, so every candidate goes to the list)"""
+    ds = dataset(2500, 64, 32, 40, "normalized")
+    for max_it in (1, 2, 3, 17, 100):
+        for K in (10, 100):
+            assert_same(*run_both(ds, "rabitq", K, topk, max_it=max_it),
+                        f"rabitq topk={topk} max_it={max_it} K={K}")
+    small = dataset(600, 32, 24, 20, "mixture")
+    assert_same(*run_both(small, "rabitq", 100, topk), f"rabitq n=600 topk={topk}")
+
+
 @pytest.mark.parametrize("degree", [48, 64, 100])
 @pytest.mark.parametrize("ny", [1, 4])
 def test_bloom_rounds_small_filters(gpu, degree, ny):
