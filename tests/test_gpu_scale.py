@@ -1,4 +1,5 @@
-"""Parity at the benchmarks' own sizes: config B (1M x 128 fp32 64-centre mixture, 10k queries,
+"""Parity at the benchmarks' own sizes: config A (100k x 128, 1k queries, topk 64, every query
+also against the restated reference CPU search), config B (1M x 128 fp32 64-centre mixture, 10k queries,
 degree-32 Vamana, base mode, topk 256, K 100), config C (the same index with the RaBitQ
 codebook, topk 768, K 10), config D (1.2M x 100 normalised N(0,1), degree 64, warp1 and bwarp2,
 topk 128, K 10) and config E (1M x 960 256-centre mixture, 1k queries, base and rabitq with
@@ -73,6 +74,30 @@ def test_config_c_rabitq_full_launch_matches_oracle(config_b):
     oi = po.OracleIndex(base, edges, codes, factors, signs)
     oids, od, ost = oi.search(queries[SAMPLE], 10, po.RABITQ_GPU, 768, erq, 1024, 1024, 0, po.L2_WAVE)
     compare(ids, d, pq, oids, od, ost, "rabitq topk 768")
+
+
+def test_config_a_every_query_matches_oracle_and_cpu_reference(gpu):
+    """config A (100k x 128 64-centre mixture, 1k queries, degree 32, topk 64, K 10, filter 1024,
+    reset 16): every query of the launch equals the oracle's GPU semantics, and since the table
+    cannot fill between resets there (1024 >= 64 + 16 x 32), also the restated reference CPU
+    search (ids, distances, expansions), which is pinned to the reference cpu_cli"""
+    base = host.gen_mixture(100_000, DIM, 64, 0.0, 128.0, 12.0, 0.0, 101, 202)
+    queries = host.gen_mixture(1000, DIM, 64, 0.0, 128.0, 12.0, 0.0, 101, 303)
+    edges = search.build_vamana_device(base, R, 128, 2.0, 1234)
+    g = search.GPUGraph(base, edges)
+    entry = g.entry_point()
+    ids, d, pq = run_device(g, queries, 10, "base", GPUBaseSearchCfg(64, 1024, entry, 1024, 16))
+    oi = po.OracleIndex(base, edges)
+    every = np.arange(1000)
+    oids, od, ost = oi.search(queries, 10, po.BASE_HASH, 64, entry, 1024, 1024, 16, po.L2_WAVE)
+    compare(ids, d, pq, oids, od, ost, "base config A", sample=every)
+    # the CPU search in the kernel's summation order: ids, distances and expansions
+    cids, cd, cst = oi.search(queries, 10, po.BASE_CPUREF, 64, entry, 1024, 1024, 16, po.L2_WAVE)
+    assert np.array_equal(ids, cids) and d.tobytes() == cd.tobytes()
+    assert np.array_equal(pq[:, 1], cst[:, 1])
+    # and in the reference's sequential order (cpu_cli's own arithmetic): the same ids here
+    sids, _, _ = oi.search(queries, 10, po.BASE_CPUREF, 64, entry, 1024, 1024, 16, po.L2_SEQ)
+    assert np.array_equal(ids, sids)
 
 
 @pytest.fixture(scope="module")
