@@ -679,7 +679,9 @@ extern "C" int bs_search(bs_index ix, const bs_search_cfg* cfg, const float* que
     hipError_t e = hipMemcpy(dq, queries, qb, hipMemcpyHostToDevice);
     if (e != hipSuccess) return fail(BS_EHIP, std::string("query upload failed: ") + hipGetErrorString(e));
     bs_stats st;
-    rc = bs_search_device(ix, cfg, dq, nq, dr, dd, dp, nullptr, 1, &st);
+    // per-query counters only when the caller asks for statistics (they cost the RaBitQ loop
+    // an expanded-set lookup of every neighbour)
+    rc = bs_search_device(ix, cfg, dq, nq, dr, dd, stats ? dp : nullptr, nullptr, 1, &st);
     if (rc == BS_OK) {
         e = hipMemcpy(results, dr, rb, hipMemcpyDeviceToHost);
         if (e == hipSuccess && dists) e = hipMemcpy(dists, dd, rb, hipMemcpyDeviceToHost);

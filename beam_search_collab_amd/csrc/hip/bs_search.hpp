@@ -388,17 +388,26 @@ search_kernel(const SearchParams p) {
 #pragma unroll
                 for (int rc = 0; rc < CR; ++rc) raw[rc] = raw_quad(pl, cw[rc < NC ? rc : 0]);
             }
+            // Only neighbours below the beam's last key can enter it (the merge drops the
+            // others first), so only they are looked up in the expanded set.  The estimate
+            // counter (neighbours not yet expanded: the reference's estimates) needs every
+            // neighbour's lookup; it is made only when per-query counters are requested.
             uint64_t ck[CR], cm[CR];
             uint32_t nv = 0;
+            const uint64_t thr_k = readlane64(beam_reg<TR>(beam, (T - 1) >> 6), (T - 1) & 63u);
+            const bool count_all = p.per_query != nullptr;
 #pragma unroll
             for (int rc = 0; rc < CR; ++rc) {
                 const uint32_t i = static_cast<uint32_t>(rc) * 64u + lane;
-                uint64_t ok = ballot(i < p.R && child[rc] != INVALID);
-                ok &= ~hf.contains_mask(child[rc], ok);
+                const uint64_t ok = ballot(i < p.R && child[rc] != INVALID);
                 const float est = estimate(raw[rc], qo.sum_q, qo.width, qo.low, ftx[rc], ffd[rc], ffv[rc], exact);
-                ck[rc] = bsw::lane_in(ok) ? make_key(est, child[rc]) : EMPTY_KEY;
-                cm[rc] = ok;
-                nv += static_cast<uint32_t>(__builtin_popcountll(cm[rc]));
+                const uint64_t key = make_key(est, child[rc]);
+                const uint64_t below = ok & ballot(key < thr_k);
+                const uint64_t probe = count_all ? ok : below;
+                const uint64_t fresh = probe ? probe & ~hf.contains_mask(child[rc], probe) : 0ull;
+                ck[rc] = bsw::lane_in(below & fresh) ? key : EMPTY_KEY;
+                cm[rc] = below & fresh;
+                nv += static_cast<uint32_t>(__builtin_popcountll(fresh));
             }
             wave_sync();
             n_est += nv;

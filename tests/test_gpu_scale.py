@@ -29,7 +29,7 @@ def config_b(gpu):
     return base, queries, edges, g
 
 
-def run_device(g, queries, K, mode, cfg):
+def run_device(g, queries, K, mode, cfg, counters=True):
     import torch
     NQ = queries.shape[0]
     dev = torch.device("cuda:0")
@@ -38,7 +38,7 @@ def run_device(g, queries, K, mode, cfg):
     dist = torch.empty((NQ, K), dtype=torch.float32, device=dev)
     pq = torch.zeros((NQ, 5), dtype=torch.int32, device=dev)
     g.search_device(q_t.data_ptr(), NQ, res.data_ptr(), K, mode, cfg, d_dists=dist.data_ptr(),
-                    d_per_query=pq.data_ptr(), sync=True)
+                    d_per_query=pq.data_ptr() if counters else 0, sync=True)
     return (res.cpu().numpy().astype(np.uint32), dist.cpu().numpy(), pq.cpu().numpy().astype(np.uint64))
 
 
@@ -70,10 +70,14 @@ def test_config_c_rabitq_full_launch_matches_oracle(config_b):
     base, queries, edges, g = config_b
     erq, codes, factors, signs = g.build_rabitq(12345)
     g.attach_rabitq(codes, factors, signs)
-    ids, d, pq = run_device(g, queries, 10, "rabitq", GPURabitqSearchCfg(768, 1024, erq, 1024))
+    cfg = GPURabitqSearchCfg(768, 1024, erq, 1024)
+    ids, d, pq = run_device(g, queries, 10, "rabitq", cfg)
     oi = po.OracleIndex(base, edges, codes, factors, signs)
     oids, od, ost = oi.search(queries[SAMPLE], 10, po.RABITQ_GPU, 768, erq, 1024, 1024, 0, po.L2_WAVE)
     compare(ids, d, pq, oids, od, ost, "rabitq topk 768")
+    # the launch without per-query counters (the benchmark's) returns the same for every query
+    ids2, d2, _ = run_device(g, queries, 10, "rabitq", cfg, counters=False)
+    assert np.array_equal(ids, ids2) and d.tobytes() == d2.tobytes()
 
 
 def test_config_a_every_query_matches_oracle_and_cpu_reference(gpu):

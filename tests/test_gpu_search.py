@@ -295,6 +295,28 @@ def test_rabitq_deferred_merge(gpu, dim, degree, kind, topk, cap):
     assert_same(*run_both(ds, "rabitq", 10, topk, cap=cap), f"rabitq d={dim} R={degree} topk={topk} cap={cap}")
 
 
+@pytest.mark.parametrize("topk", [64, 256, 512, 768])
+@pytest.mark.parametrize("degree", [24, 100])
+def test_rabitq_counters_change_no_result(gpu, topk, degree):
+    """with per-query counters the RaBitQ loop looks every neighbour up in the expanded set (to
+    count the estimates); without them only the neighbours below the beam's last key.  Ids and
+    distances must be the oracle's either way"""
+    import torch
+    ds = dataset(2500, 64, degree, 40, "normalized")
+    cfg = GPURabitqSearchCfg(topk, 256, ds["erq"], 1024)
+    oids, od, _ = ds["oi"].search(ds["q"], 10, OMODE["rabitq"], topk, ds["erq"], 1024, 256, 0, po.L2_WAVE)
+    dev = torch.device("cuda:0")
+    q_t = torch.from_numpy(ds["q"]).to(dev)
+    for counters in (True, False):
+        res = torch.empty((40, 10), dtype=torch.int32, device=dev)
+        dist = torch.empty((40, 10), dtype=torch.float32, device=dev)
+        pq = torch.zeros((40, 5), dtype=torch.int32, device=dev)
+        ds["g"].search_device(q_t.data_ptr(), 40, res.data_ptr(), 10, "rabitq", cfg, d_dists=dist.data_ptr(),
+                              d_per_query=pq.data_ptr() if counters else 0, sync=True)
+        assert np.array_equal(res.cpu().numpy().astype(np.uint32), oids), (topk, degree, counters)
+        assert dist.cpu().numpy().tobytes() == od.tobytes(), (topk, degree, counters)
+
+
 @pytest.mark.parametrize("topk", [513, 768, 1024])
 def test_rabitq_deferred_merge_iteration_limits(gpu, topk):
     """the deferred merge when the loop ends by max_iterations with keys still in the list
