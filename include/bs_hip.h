@@ -97,7 +97,8 @@ int bs_index_attach_rabitq(bs_index idx, const uint32_t* codes, const float* fac
 /* Search nq host-resident queries (nq*dim f32); results (host, nq*K u32) and optional
  * dists (host, nq*K f32, NULL allowed) are written.  Replaces one timed launch of
  * run_base / run_warp / run_rabitq (src/gpu_cli.cu:140-349) including the query upload
- * and result download of gpu_cli main (src/gpu_cli.cu:399-421,481). stats nullable.
+ * and result download of gpu_cli main (src/gpu_cli.cu:399-421,481). stats nullable; with
+ * stats the per-query counters are collected too (see bs_search_device).
  * The device staging buffers belong to the index: they grow to the largest call and are
  * reused (freed by bs_index_destroy). */
 int bs_search(bs_index idx, const bs_search_cfg* cfg, const float* queries, uint64_t nq,
@@ -107,7 +108,10 @@ int bs_search(bs_index idx, const bs_search_cfg* cfg, const float* queries, uint
  * dists nq*K f32 or NULL, per_query nq*5 u32 counters {iterations, expansions,
  * dist_evals, est_evals, rerank_evals} or NULL), launched on `stream` (hipStream_t or
  * NULL).  Allocates no device memory.  Asynchronous unless sync != 0; with sync != 0
- * stats (nullable) gets kernel_ms and, when per_query is given, the summed counters. */
+ * stats (nullable) gets kernel_ms and, when per_query is given, the summed counters.
+ * Results never depend on per_query; in rabitq mode it costs an expanded-set lookup of
+ * every neighbour (to count est_evals), which the search itself needs only for the
+ * neighbours below the beam's last key, so pass NULL where counters are not wanted. */
 int bs_search_device(bs_index idx, const bs_search_cfg* cfg, const float* d_queries,
                      uint64_t nq, uint32_t* d_results, float* d_dists, uint32_t* d_per_query,
                      void* stream, int sync, bs_stats* stats);
