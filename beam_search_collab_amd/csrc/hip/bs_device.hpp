@@ -303,8 +303,10 @@ __device__ __forceinline__ void beam_merge(uint64_t (&beam)[TR], const uint64_t 
     wave_sync();
 #pragma unroll
     for (int r = 0; r < TR; ++r) beam[r] = lds_scratch[static_cast<uint32_t>(r) * 64u + lane];
-    if constexpr (SPLIT) {
-        // lane r: slot 64 r + 63 (EMPTY at T and beyond)
+    if constexpr (merge_split<TR, 1>()) {
+        // lane r: slot 64 r + 63 (EMPTY at T and beyond).  Refreshed whenever a later
+        // one-register merge of this beam may rank by st.last, also after a merge that did
+        // not use it (four candidate registers: the deferred merge's direct path)
         const uint64_t lk = lds_scratch[min(64u * lane + 63u, DUMP)];
         st.last = bsw::lane_in(last_live<TR>(T)) ? lk : EMPTY_KEY;
     }

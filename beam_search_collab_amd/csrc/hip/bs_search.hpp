@@ -423,7 +423,10 @@ search_kernel(const SearchParams p) {
 #pragma unroll
         for (int r = 0; r < TR; ++r) {
             const uint32_t e = static_cast<uint32_t>(r) * 64u + lane;
-            ids[e] = (beam[r] == EMPTY_KEY) ? INVALID : key_id(beam[r]);
+            // an empty slot names row 0: the gather below reads the first nvb ids, which
+            // are all valid while the beam is sorted (empty keys last); should that order
+            // ever break, the rerank reads a wrong row instead of one outside the index
+            ids[e] = (beam[r] == EMPTY_KEY) ? 0u : key_id(beam[r]);
             nvb += static_cast<uint32_t>(__builtin_popcountll(ballot(beam[r] != EMPTY_KEY)));
         }
         wave_sync();

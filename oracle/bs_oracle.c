@@ -28,8 +28,12 @@
  *                    new); reduces to ORC_BASE_HASH when the filter has no false positives.
  *   ORC_RABITQ_GPU   ids, order and distances of the reference cpu_cli rabitq search on the
  *                    inputs where the two searches must coincide (fdq = fvq = 0, a tree padded
- *                    with self-loops, integer vectors; tests/golden/rqtree_*); properties
- *                    (exact rerank, sorted, deduplicated) and recall elsewhere.
+ *                    with self-loops, integer vectors; tests/golden/rqtree_*); the
+ *                    expanded-set re-entry, the skip of a node expanded before, node-0
+ *                    padding, evictions, the rerank and the dedup flush by a 9-node search
+ *                    traced by hand (tests/test_rabitq_hand_trace.py: ids, distances and
+ *                    every counter as literals), which each planted mistake of the
+ *                    ORC_MUTANTS build fails; properties and recall elsewhere.
  *   orc_entry_point  reference cpu_cli "entry=" line (bit-exact id).
  *   orc_beam_run, orc_filter_run
  *                    closed forms of the reference unit tests (shuffled 0..n-1 keep the
@@ -654,6 +658,19 @@ static void search_base_cpuref(const orc_index* ix, const orc_cfg* cfg, const fl
  * re-enter the beam through another parent) -> merge.  Then exact-L2 rerank of every
  * beam slot (:315-317), sort, and a dedup flush from the smallest (:320-339) that
  * accepts at most `filter size` distinct ids. */
+#ifdef ORC_MUTANTS
+/* Planted mistakes, built only into bin/libbs_oracle_mutant.so: the tests check that a
+ * fixture fails each of them (a fixture that a plausible misreading passes pins nothing).
+ *   1  a node is seen once it enters the beam (cpu_search_rabitq.hpp:128-133) instead of
+ *      once it is expanded: no second estimate through another parent
+ *   2  a picked node that was expanded before is expanded again (no skip, :250-252)
+ *   3  the flush writes duplicate ids (no dedup, :320-339) */
+int orc_mutant = 0;
+#define MUTANT(k) (orc_mutant == (k))
+#else
+#define MUTANT(k) 0
+#endif
+
 static void search_rabitq_gpu(const orc_index* ix, const orc_cfg* cfg, const float* q,
                               uint32_t* res, float* dists, orc_stats* st) {
     const int R = ix->degree, dim = ix->dim;
@@ -672,12 +689,15 @@ static void search_rabitq_gpu(const orc_index* ix, const orc_cfg* cfg, const flo
     uint64_t e = orc_make_key(l2_of(cfg->l2_kind, q, ix->vecs + (size_t)ep * dim, dim), ep, 0);
     st->dist_evals++;
     beam_merge(&b, &e, 1);
+    hashf seen; /* mutant 1 only */
+    hash_init(&seen, MUTANT(1) ? 1u << 20 : 1u);
+    if (MUTANT(1)) hash_insert(&seen, ep);
 
     for (int32_t iter = 0; iter < cfg->max_iterations; ++iter) {
         st->iterations++;
         uint32_t p = beam_pick(&b, 1);
         if (p == ORC_INVALID_ID) break;
-        if (!hash_insert(&h, p)) continue;
+        if (!hash_insert(&h, p) && !MUTANT(2)) continue;
         st->expansions++;
         float exact = l2_of(cfg->l2_kind, q, ix->vecs + (size_t)p * dim, dim);
         st->dist_evals++;
@@ -688,6 +708,7 @@ static void search_rabitq_gpu(const orc_index* ix, const orc_cfg* cfg, const flo
         for (int i = 0; i < R; ++i) {
             uint32_t child = row[i];
             if (child == ORC_INVALID_ID || hash_contains(&h, child)) continue;
+            if (MUTANT(1) && !hash_insert(&seen, child)) continue;
             uint32_t raw = orc_raw_dot(codes, pc + (size_t)i * wpp, pdim);
             float est = orc_estimate(raw, sum_q, width, low, fac[i], fac[R + i], fac[2 * R + i], exact);
             st->est_evals++;
@@ -710,7 +731,7 @@ static void search_rabitq_gpu(const orc_index* ix, const orc_cfg* cfg, const flo
     uint32_t written = 0, distinct = 0, prev = ORC_INVALID_ID;
     for (uint32_t i = 0; i < nv && written < cfg->K; ++i) {
         uint32_t id = key_id(cand[i]);
-        if (id == prev) continue;
+        if (id == prev && !MUTANT(3)) continue;
         prev = id;
         if (distinct >= h.size) continue;
         distinct++;
@@ -725,6 +746,7 @@ static void search_rabitq_gpu(const orc_index* ix, const orc_cfg* cfg, const flo
     free(codes);
     free(cand);
     hash_free(&h);
+    hash_free(&seen);
     beam_free(&b);
 }
 

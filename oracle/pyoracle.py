@@ -74,6 +74,26 @@ def lib():
     return _lib
 
 
+MUTANT_PATH = os.path.join(HERE, "bin", "libbs_oracle_mutant.so")
+MUTANT_SEEN_AT_ENTRY, MUTANT_REEXPAND, MUTANT_NO_DEDUP = 1, 2, 3
+_mlib = None
+
+
+def mutant_search(index, queries, K, mutant, topk, entry, max_it=1024, cap=1024):
+    """ORC_RABITQ_GPU of the oracle built with a planted mistake (bs_oracle.c, ORC_MUTANTS):
+    for tests that show a fixture tells the mistake apart"""
+    global _mlib
+    if _mlib is None:
+        if not os.path.exists(MUTANT_PATH):
+            raise ImportError(f"{MUTANT_PATH} missing: make -C oracle")
+        _mlib = C.CDLL(MUTANT_PATH)
+        _mlib.orc_search.restype = C.c_int
+        _mlib.orc_search.argtypes = [C.POINTER(Index), C.POINTER(Cfg), C.c_void_p, C.c_uint64, C.c_void_p,
+                                     C.c_void_p, C.c_void_p]
+    C.c_int.in_dll(_mlib, "orc_mutant").value = int(mutant)
+    return index.search(queries, K, RABITQ_GPU, topk, entry, max_it, cap, 0, L2_WAVE, _lib_handle=_mlib)
+
+
 def _p(a):
     return a.ctypes.data_as(C.c_void_p)
 
@@ -153,14 +173,14 @@ class OracleIndex:
             ix.padded_dim = self.signs.shape[0]
         self.ix = ix
 
-    def search(self, queries, K, mode, topk, entry, max_it=1024, cap=1024, reset=16, l2=L2_WAVE):
+    def search(self, queries, K, mode, topk, entry, max_it=1024, cap=1024, reset=16, l2=L2_WAVE, _lib_handle=None):
         q = np.ascontiguousarray(queries, np.float32)
         nq = q.shape[0]
         c = Cfg(mode, l2, K, topk, cap, entry, max_it, reset)
         res = np.empty((nq, K), np.uint32)
         d = np.empty((nq, K), np.float32)
         st = (Stats * nq)()
-        rc = lib().orc_search(C.byref(self.ix), C.byref(c), _p(q), nq, _p(res), _p(d), C.cast(st, C.c_void_p))
+        rc = (_lib_handle or lib()).orc_search(C.byref(self.ix), C.byref(c), _p(q), nq, _p(res), _p(d), C.cast(st, C.c_void_p))
         if rc != 0:
             raise ValueError("orc_search failed")
         stats = np.array([[s.iterations, s.expansions, s.dist_evals, s.est_evals, s.rerank_evals] for s in st],

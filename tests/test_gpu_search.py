@@ -331,6 +331,39 @@ def test_rabitq_deferred_merge_iteration_limits(gpu, topk):
     assert_same(*run_both(small, "rabitq", 100, topk), f"rabitq n=600 topk={topk}")
 
 
+@functools.lru_cache(maxsize=None)
+def ragged_dataset(n, dim, degree, nq, seed):
+    """random rows that alternate by node parity between many valid neighbours (more than 64:
+    the deferred merge takes them directly, through four candidate registers) and 1-4 valid
+    neighbours (appended to the pending list), the rest of each row absent"""
+    rng = np.random.default_rng(seed)
+    base = host.gen_normalized(n, dim, seed + 1)
+    q = host.gen_normalized(nq, dim, seed + 2)
+    edges = np.full((n, degree), po.INVALID_ID, np.uint32)
+    for i in range(n):
+        cnt = int(rng.integers(100, degree + 1)) if i % 2 == 0 else int(rng.integers(1, 5))
+        edges[i, :cnt] = rng.choice(n, cnt, replace=False)
+    erq, codes, factors, signs = host.build_rabitq(base, edges, 12345)
+    g = search.GPUGraph(base, edges)
+    g.attach_rabitq(codes, factors, signs)
+    oi = po.OracleIndex(base, edges, codes, factors, signs)
+    return dict(base=base, q=q, edges=edges, g=g, oi=oi, entry=erq, erq=erq)
+
+
+@pytest.mark.parametrize("dim", [64, 160])
+@pytest.mark.parametrize("topk", [768, 1024])
+def test_rabitq_deferred_merge_ragged_rows(gpu, dim, topk):
+    """beams of 12 and 16 registers at degree 256 (four candidate registers): a dense row's
+    direct merge followed by a flush of 1-4 list keys.  The flush ranks its keys by the
+    registers' last keys, which the direct merge must leave current; max_iterations that end
+    the loop right after such a merge (the final flush) and full searches"""
+    ds = ragged_dataset(3000, dim, 256, 32, 21)
+    assert int((ds["edges"] != po.INVALID_ID).sum(1).max()) > 128
+    for max_it in (2, 3, 5, 12, 40, 1024):
+        assert_same(*run_both(ds, "rabitq", 10, topk, max_it=max_it), f"ragged d={dim} topk={topk} max_it={max_it}")
+    assert_same(*run_both(ds, "rabitq", 100, topk, cap=256), f"ragged d={dim} topk={topk} cap=256")
+
+
 @pytest.mark.parametrize("degree", [48, 64, 100])
 @pytest.mark.parametrize("ny", [1, 4])
 def test_bloom_rounds_small_filters(gpu, degree, ny):
