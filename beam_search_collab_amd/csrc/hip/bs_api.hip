@@ -397,7 +397,10 @@ int make_plan(bs_index ix, const bs_search_cfg* cfg, uint64_t nq, Plan& pl) {
     if (cap > (1u << 22)) return fail(BS_EINVAL, "filter_capacity must be <= 2^22");
 
     pl.mode = mode;
-    pl.TR = T <= 64 ? 1 : T <= 128 ? 2 : T <= 256 ? 4 : T <= 512 ? 8 : (T <= 768 && mode == BS_RABITQ) ? 12 : 16;
+    // RaBitQ beams of 513..640 and 641..768 keys get 10 and 12 registers (the recall@10 0.95
+    // point of config C is topk 640: 1M x 128, 10k queries, 6.31 ms with 12 registers)
+    pl.TR = T <= 64 ? 1 : T <= 128 ? 2 : T <= 256 ? 4 : T <= 512 ? 8
+          : (T <= 640 && mode == BS_RABITQ) ? 10 : (T <= 768 && mode == BS_RABITQ) ? 12 : 16;
     pl.CR = ix->degree <= 64 ? 1 : ix->degree <= 128 ? 2 : 4;
     bsd::L2Shape L = bsd::l2_shape(ix->dim);
     if (L.QR > 4) return fail(BS_EINVAL, "dim too large");
@@ -457,10 +460,9 @@ int make_plan(bs_index ix, const bs_search_cfg* cfg, uint64_t nq, Plan& pl) {
         if (mode == BS_RABITQ) p.off_planes = planes_rel + p.off_scratch;
         p.off_coop = p.off_cand + 64u * pl.CR * 8u + 8u * std::max(pl.TR, 8);  // after the merge's slot bitmap
         p.lds_wave = al(p.off_coop + 4u);
-        if (mode == BS_RABITQ && pl.TR >= 8) {  // the deferred merge's pending list
-            p.off_pend = p.lds_wave;
-            p.lds_wave += 64u * 8u;
-        }
+        // the deferred merge's append staging (64 keys) reuses the merge scratch: it is
+        // written and read back inside pending_add, where no merge is running
+        if (mode == BS_RABITQ && pl.TR >= 8) p.off_pend = p.off_scratch;
     };
     if (mode == BS_GROUP_BLOOM) {
         uint32_t b = log2_ceil(cap);
@@ -487,9 +489,23 @@ int make_plan(bs_index ix, const bs_search_cfg* cfg, uint64_t nq, Plan& pl) {
             }
         } else {
             // the expanded set holds about one key per beam slot: 5T/3 slots (a multiple of
-            // 64), at least cap and at most 2 cap
+            // 64), at least cap and at most 2 cap, and no more than the LDS that the
+            // instance's register-limited residency leaves (fewer slots rather than fewer
+            // wavefronts per CU)
             const uint64_t want = (5ull * T / 3 + 63) / 64 * 64;
             p.filter_slots = static_cast<uint32_t>(std::min<uint64_t>(2ull * base_slots, std::max<uint64_t>(base_slots, want)));
+            layout(0);
+            const uint32_t other = p.lds_wave;
+            int wg = 0;
+            const hipError_t oe =
+                ix->wpp <= 4 ? bsd::launch_search_rabitq(p, pl.TR, pl.CR, pl.PB, dim3(1), dim3(64), 0, nullptr, &wg)
+                             : bsd::launch_search_rabitq_wide(p, pl.TR, pl.CR, pl.PB, dim3(1), dim3(64), 0, nullptr, &wg);
+            if (oe == hipSuccess && wg > 0) {
+                const uint32_t per_wave =
+                    static_cast<uint32_t>((ix->lds_cu / static_cast<size_t>(wg)) & ~static_cast<size_t>(LDS_GRANULE - 1));
+                const uint32_t fit = per_wave > other ? (per_wave - other) / 4u / 64u * 64u : 0u;
+                if (fit < p.filter_slots) p.filter_slots = std::max(base_slots, fit);
+            }
         }
         layout(p.filter_slots * 4u);
         if (static_cast<size_t>(p.lds_wave) * ny > ix->max_lds && p.filter_slots > base_slots) {

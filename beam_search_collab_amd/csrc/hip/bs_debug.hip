@@ -218,7 +218,7 @@ __global__ void __launch_bounds__(64) dbg_beam_kernel(uint32_t T, const uint64_t
     uint64_t beam[TR];
 #pragma unroll
     for (int r = 0; r < TR; ++r) beam[r] = bsd::EMPTY_KEY;
-    bsd::BeamState st = {0u, bsd::EMPTY_KEY};  // kept by merge and pick
+    bsd::BeamState st = {0u};  // kept by merge and pick
     for (uint32_t b = 0; b < nbatch; ++b) {
         uint64_t ck[CR], cm[CR];
 #pragma unroll
@@ -269,13 +269,17 @@ extern "C" int bs_debug_beam(uint32_t topk, const uint64_t* keys, uint32_t nbatc
     DTRY(db.alloc(topk));
     DTRY(dp.alloc(static_cast<size_t>(nbatch) * picks));
     if (nk) DTRY(hipMemcpy(dk.p, keys, nk * 8, hipMemcpyHostToDevice));
-    const int TR = topk <= 64 ? 1 : topk <= 128 ? 2 : topk <= 256 ? 4 : topk <= 512 ? 8 : 16;
+    // the search kernel's beam sizes, with the RaBitQ ones (10 and 12 registers) above 512
+    const int TR = topk <= 64 ? 1 : topk <= 128 ? 2 : topk <= 256 ? 4 : topk <= 512 ? 8 : topk <= 640 ? 10
+                 : topk <= 768 ? 12 : 16;
     const int CR = bsize <= 64 ? 1 : 2;
     switch (TR) {
     case 1: launch_beam_c<1>(CR, pick_run, topk, dk.p, nbatch, bsize, picks, dp.p, db.p); break;
     case 2: launch_beam_c<2>(CR, pick_run, topk, dk.p, nbatch, bsize, picks, dp.p, db.p); break;
     case 4: launch_beam_c<4>(CR, pick_run, topk, dk.p, nbatch, bsize, picks, dp.p, db.p); break;
     case 8: launch_beam_c<8>(CR, pick_run, topk, dk.p, nbatch, bsize, picks, dp.p, db.p); break;
+    case 10: launch_beam_c<10>(CR, pick_run, topk, dk.p, nbatch, bsize, picks, dp.p, db.p); break;
+    case 12: launch_beam_c<12>(CR, pick_run, topk, dk.p, nbatch, bsize, picks, dp.p, db.p); break;
     default: launch_beam_c<16>(CR, pick_run, topk, dk.p, nbatch, bsize, picks, dp.p, db.p); break;
     }
     DTRY(hipGetLastError());

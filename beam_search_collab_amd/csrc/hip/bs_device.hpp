@@ -56,10 +56,8 @@ __device__ __forceinline__ uint32_t key_id(uint64_t k) { return static_cast<uint
 // lands at position >= T and is evicted (ties go after beam entries), so it is dropped
 // first.  The beam stays sorted (a mark sets a key's LSB: beam_pick marks the last of a
 // run of identical keys).  Two ways to the same result:
-//  - rank loop: each remaining candidate kj is broadcast once.  The registers whose last
-//    key is <= kj keep their elements, register rs = #(such registers) holds kj's
-//    insertion point (its elements > kj shift by one: one compare), every later register
-//    shifts by one as a whole (a scalar count);
+//  - rank loop: each remaining candidate kj is broadcast once and compared with every beam
+//    register (the compare mask is the ballot): the elements above kj shift by one;
 //  - sorted merge (CR = 1, SORTED, at least merge_sort_min<TR>() candidates): the candidates are
 //    compacted and bitonic-sorted across lanes, each finds its rank in the beam by a
 //    binary search of an LDS copy, the occupied output slots are marked in a bitmap and
@@ -68,20 +66,19 @@ __device__ __forceinline__ uint32_t key_id(uint64_t k) { return static_cast<uint
 // LDS: scratch = 64*TR + 1 keys (the last one a dump slot), aux = 64 + TR keys.
 // ---------------------------------------------------------------------------
 // What merge and pick keep besides the registers: `first`, a lower bound on the register
-// that holds the first unexpanded key (0 always is one), and `last`, lane r < TR holding
-// the last key of register r (element 64 r + 63), EMPTY in the lanes beyond.
+// that holds the first unexpanded key (0 always is one).  (Finding a candidate's register
+// from the registers' last keys instead of comparing it with every register was measured
+// slower for every beam size once the large RaBitQ beams defer their merges: 1M x 128, 10k
+// queries, rabitq topk 600 5.91 -> 5.60 ms, 768 7.69 -> 6.77, 1024 11.0 -> 9.19 ms without
+// it; base topk 1024 unchanged.)
 struct BeamState {
     uint32_t first;
-    uint64_t last;
 };
 
 template <int TR>
-__device__ __forceinline__ BeamState beam_state(const uint64_t (&beam)[TR]) {
+__device__ __forceinline__ BeamState beam_state(const uint64_t (&)[TR]) {
     BeamState st;
     st.first = 0;
-    st.last = EMPTY_KEY;
-#pragma unroll
-    for (int r = 0; r < TR; ++r) st.last = bsw::lane_in(1ull << r) ? readlane64(beam[r], 63) : st.last;
     return st;
 }
 
@@ -91,23 +88,8 @@ __device__ __forceinline__ uint64_t beam_reg(const uint64_t (&beam)[TR], uint32_
     return beam[r];
 }
 
-// lanes r < TR whose register's last slot 64 r + 63 lies below T
-template <int TR>
-__device__ __forceinline__ uint64_t last_live(uint32_t T) {
-    const uint32_t full = T >> 6;  // registers with every slot below T
-    const uint32_t n = full < static_cast<uint32_t>(TR) ? full : static_cast<uint32_t>(TR);
-    return n >= 64u ? ~0ull : (1ull << n) - 1ull;
-}
-
-// The rank loop finds a candidate's register from the registers' last keys (beams of 12
-// or more registers; ~8 instructions per candidate, plus the last keys' upkeep) or by
-// comparing it with every register (smaller beams; ~2 TR + 6).  The sorted merge's fixed
-// cost (~250 instructions plus LDS latency) against the rank loop's: the crossover.
-template <int TR, int CR>
-__device__ __forceinline__ constexpr bool merge_split() {
-    return TR >= 12 && CR <= 3;  // 8-bit split counts: at most 192 candidates
-}
-
+// The rank loop costs ~2 TR + 6 instructions per candidate, the sorted merge ~250 plus LDS
+// latency: the crossover.
 template <int TR>
 __device__ __forceinline__ constexpr uint32_t merge_sort_min() {
     return TR >= 16 ? 3u : TR >= 8 ? 5u : 8u;
@@ -200,17 +182,6 @@ __device__ __forceinline__ void beam_merge_sorted(uint64_t (&beam)[TR], uint64_t
         before += static_cast<uint32_t>(__builtin_popcountll(mw));
     }
     beam_clear_tail<TR>(beam, T);
-    if constexpr (merge_split<TR, 1>()) {
-        // the registers' last keys into lanes 0..TR-1, through C (free once gathered; the
-        // wave's LDS accesses complete in order)
-        if (lane == 63u) {
-#pragma unroll
-            for (int r = 0; r < TR; ++r) C[r] = beam[r];
-        }
-        wave_sync();
-        const uint64_t lk = C[lane < static_cast<uint32_t>(TR) ? lane : 0u];
-        st.last = lane < static_cast<uint32_t>(TR) ? lk : EMPTY_KEY;
-    }
     wave_sync();
 }
 
@@ -234,15 +205,10 @@ __device__ __forceinline__ void beam_merge(uint64_t (&beam)[TR], const uint64_t 
             return;
         }
     }
-    constexpr bool SPLIT = merge_split<TR, CR>();
-    // lp[r]: per-lane shift of register r (SPLIT: by the candidates whose insertion point is
-    // inside it; otherwise: by every smaller candidate); nsplit (SPLIT): 8-bit counts of
-    // those candidates per register (registers 0-7, 8-15), from which the later registers'
-    // whole-register shifts follow
+    // lp[r]: per-lane shift of register r, by every smaller candidate
     uint32_t lp[TR];
 #pragma unroll
     for (int r = 0; r < TR; ++r) lp[r] = 0;
-    uint64_t nsplit0 = 0, nsplit1 = 0;
     uint32_t cpos[CR];
 #pragma unroll
     for (int rc = 0; rc < CR; ++rc) cpos[rc] = 0;
@@ -255,26 +221,14 @@ __device__ __forceinline__ void beam_merge(uint64_t (&beam)[TR], const uint64_t 
             const uint32_t lj = static_cast<uint32_t>(__builtin_ctzll(m));
             m &= m - 1;
             const uint64_t kj = readlane64(ck[rj], lj);
-            uint32_t le;  // #(beam <= kj)
-            if constexpr (SPLIT) {
-                // kj < thr: register (T - 1) / 64 ends above kj, so rs < TR
-                const uint32_t rs = static_cast<uint32_t>(__builtin_popcountll(ballot(st.last <= kj)));
-                const uint64_t lt = ballot(kj < beam_reg<TR>(beam, rs));
-                lp[rs] += bsw::lane_in(lt) ? 1u : 0u;
-                const uint64_t inc = 1ull << (8u * (rs & 7u));
-                nsplit0 += rs < 8u ? inc : 0ull;
-                nsplit1 += rs < 8u ? 0ull : inc;
-                le = 64u * rs + static_cast<uint32_t>(__builtin_popcountll(~lt));
-            } else {
-                uint32_t ngt = 0;
+            uint32_t ngt = 0;  // #(beam > kj)
 #pragma unroll
-                for (int r = 0; r < TR; ++r) {
-                    const uint64_t lt = ballot(kj < beam[r]);
-                    lp[r] += bsw::lane_in(lt) ? 1u : 0u;
-                    ngt += static_cast<uint32_t>(__builtin_popcountll(lt));
-                }
-                le = 64u * TR - ngt;
+            for (int r = 0; r < TR; ++r) {
+                const uint64_t lt = ballot(kj < beam[r]);
+                lp[r] += bsw::lane_in(lt) ? 1u : 0u;
+                ngt += static_cast<uint32_t>(__builtin_popcountll(lt));
             }
+            const uint32_t le = 64u * TR - ngt;  // #(beam <= kj)
             minle = min(minle, le);
 #pragma unroll
             for (int rc = 0; rc < CR; ++rc) {
@@ -291,25 +245,16 @@ __device__ __forceinline__ void beam_merge(uint64_t (&beam)[TR], const uint64_t 
     // keys landing at 64*TR or beyond go to the dump slot 64*TR, those landing in
     // [T, 64*TR) are overwritten with EMPTY after the gather (beam_clear_tail).
     constexpr uint32_t DUMP = 64u * TR;
-    uint32_t shift = 0;  // candidates inserted in earlier registers
 #pragma unroll
     for (int r = 0; r < TR; ++r) {
-        const uint32_t bpos = static_cast<uint32_t>(r) * 64u + shift + lane + lp[r];
+        const uint32_t bpos = static_cast<uint32_t>(r) * 64u + lane + lp[r];
         lds_scratch[min(bpos, DUMP)] = beam[r];
-        shift += static_cast<uint32_t>(((r < 8 ? nsplit0 : nsplit1) >> (8 * (r & 7))) & 0xFFu);
     }
 #pragma unroll
     for (int rc = 0; rc < CR; ++rc) lds_scratch[bsw::lane_in(cmask[rc]) ? min(cpos[rc], DUMP) : DUMP] = ck[rc];
     wave_sync();
 #pragma unroll
     for (int r = 0; r < TR; ++r) beam[r] = lds_scratch[static_cast<uint32_t>(r) * 64u + lane];
-    if constexpr (merge_split<TR, 1>()) {
-        // lane r: slot 64 r + 63 (EMPTY at T and beyond).  Refreshed whenever a later
-        // one-register merge of this beam may rank by st.last, also after a merge that did
-        // not use it (four candidate registers: the deferred merge's direct path)
-        const uint64_t lk = lds_scratch[min(64u * lane + 63u, DUMP)];
-        st.last = bsw::lane_in(last_live<TR>(T)) ? lk : EMPTY_KEY;
-    }
     beam_clear_tail<TR>(beam, T);
     st.first = min(st.first, minle >> 6);
     wave_sync();
@@ -377,7 +322,6 @@ __device__ __forceinline__ void beam_mark(uint64_t (&beam)[TR], BeamState& st, u
     }
     // set the mark (key LSB) of element (qr, ql)
     beam[qr] |= bsw::lane_in(1ull << ql) ? 1ull : 0ull;
-    if constexpr (merge_split<TR, 1>()) st.last |= bsw::lane_in(ql == 63u ? 1ull << qr : 0ull) ? 1ull : 0ull;
 }
 
 template <int TR, bool RUN>
@@ -434,7 +378,6 @@ __device__ __forceinline__ uint32_t beam_pick(uint64_t (&beam)[TR], BeamState& s
     }
     // set the mark (key LSB) of element (qr, ql)
     beam[qr] |= bsw::lane_in(1ull << ql) ? 1ull : 0ull;
-    if constexpr (merge_split<TR, 1>()) st.last |= bsw::lane_in(ql == 63u ? 1ull << qr : 0ull) ? 1ull : 0ull;
     return key_id(kp);
 }
 

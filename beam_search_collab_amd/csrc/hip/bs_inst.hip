@@ -59,7 +59,8 @@ static hipError_t launch_any(const SearchParams& p, int TR, int CR, int PB, dim3
     case 4: return launch_c<4>(p, CR, PB, g, b, lds, s, occ);
     case 8: return launch_c<8>(p, CR, PB, g, b, lds, s, occ);
 #if BS_INST_MODE >= 2
-    case 12: return launch_c<12>(p, CR, PB, g, b, lds, s, occ);  // rabitq beams of 513..768
+    case 10: return launch_c<10>(p, CR, PB, g, b, lds, s, occ);  // rabitq beams of 513..640
+    case 12: return launch_c<12>(p, CR, PB, g, b, lds, s, occ);  // rabitq beams of 641..768
 #endif
     default: return launch_c<16>(p, CR, PB, g, b, lds, s, occ);
     }

@@ -36,7 +36,7 @@ struct SearchParams {
     uint32_t lds_wave;      // bytes of LDS per wavefront
     uint32_t off_filter, off_scratch, off_cand;  // byte offsets inside the wave slice
     uint32_t off_planes;    // rabitq: the query's bit planes (outside the merge scratch)
-    uint32_t off_pend;      // rabitq, beams of more than 256: the deferred merge's list (64 keys)
+    uint32_t off_pend;      // rabitq, beams of more than 256: the deferred merge's append staging (64 keys, in the merge scratch)
     uint32_t coop;          // base mode: wavefronts per query (1, 2, 4); 1 otherwise
     uint32_t off_coop;      // word where the first wavefront posts the row count
     L2Shape L;
@@ -45,9 +45,13 @@ struct SearchParams {
 // Register budget per instance, matched to what the LDS slice allows anyway: RaBitQ beams
 // up to 256 (about 7 KB of LDS per wavefront) are compiled for 5 wavefronts per SIMD (at most
 // 96 VGPRs); the loops with beams up to 256 and two passes of rows in flight (Bloom over rows
-// of up to 128 dims, hash over rows of up to 64) get 4 (128 VGPRs, no spills).
+// of up to 128 dims, hash over rows of up to 64) get 4 (128 VGPRs, no spills).  RaBitQ beams
+// of 513..768 keys with narrow codes get 4 as well (left alone they take 3 per SIMD, against
+// 4 for 8 registers): 1M x 128, 10k queries, topk 704 6.52 -> 6.39 ms, 768 6.94 -> 6.77; 16
+// registers lose with it (9.19 -> 10.3 ms).
 template <int TR, int CR, int MODE, int PB>
 constexpr int min_waves_per_simd() {
+    if (MODE == MODE_RABITQ && CR == 1 && (TR == 10 || TR == 12)) return 4;
     return (CR != 1 || TR > 4) ? 1 : MODE == MODE_RABITQ ? 5 : PB == 2 ? 4 : 1;
 }
 
@@ -84,7 +88,7 @@ search_kernel(const SearchParams p) {
     for (int r = 0; r < TR; ++r) beam[r] = EMPTY_KEY;
 
     uint32_t n_iter = 0, n_exp = 0, n_dist = 0, n_est = 0, n_rr = 0;
-    BeamState st = {0u, EMPTY_KEY};  // the pick's scan start, the registers' last keys
+    BeamState st = {0u};  // the pick's scan start
 
     if constexpr (MODE == MODE_HASH || MODE == MODE_BLOOM) {
         // ------------------------------------------------------------------ base
@@ -315,7 +319,9 @@ search_kernel(const SearchParams p) {
         // keys (pending_add); 1M x 128, 10k queries: topk 768 8.87 -> 8.11 ms, 512 6.11 ->
         // 5.95, while smaller beams lose (256 2.67 -> 2.73, 128 1.47 -> 1.61)
         constexpr bool DEFER = TR >= 8;
-        PendingList pd = {DEFER ? reinterpret_cast<uint64_t*>(my + p.off_pend) : nullptr, 0u, EMPTY_KEY};  // LDS only when DEFER
+        // the list's append staging shares the merge scratch (live only between pending_add's
+        // compaction and its read-back, when no merge runs)
+        PendingList pd = {DEFER ? reinterpret_cast<uint64_t*>(my + p.off_pend) : nullptr, 0u, EMPTY_KEY};
         uint32_t picks = 0;
 
         for (int32_t iter = 0; iter < p.max_it; ++iter) {

@@ -74,7 +74,8 @@ def _keys(d, ids):
 
 
 @pytest.mark.parametrize("topk,bsize", [(16, 16), (64, 32), (100, 32), (128, 64), (256, 64), (256, 128),
-                                        (512, 64), (512, 128), (1024, 64), (1000, 128)])
+                                        (512, 64), (512, 128), (600, 64), (640, 128), (700, 64), (768, 128),
+                                        (1024, 64), (1000, 128)])
 def test_beam_merge_keeps_smallest(gpu, topk, bsize):
     rng = np.random.default_rng(topk * 7 + bsize)
     n = 4 * max(topk, bsize)
@@ -88,7 +89,7 @@ def test_beam_merge_keeps_smallest(gpu, topk, bsize):
 
 
 @pytest.mark.parametrize("topk,bsize,picks", [(64, 32, 1), (128, 32, 2), (256, 64, 1), (512, 64, 3),
-                                              (100, 16, 2), (1024, 64, 2)])
+                                              (100, 16, 2), (600, 64, 2), (768, 32, 3), (1024, 64, 2)])
 def test_beam_interleaved_pick_no_dup_and_order(gpu, topk, bsize, picks):
     rng = np.random.default_rng(topk + picks)
     n = 8 * topk

@@ -328,7 +328,7 @@ def test_rabitq_counters_change_no_result(gpu, topk, degree):
         assert dist.cpu().numpy().tobytes() == od.tobytes(), (topk, degree, counters)
 
 
-@pytest.mark.parametrize("topk", [513, 768, 1024])
+@pytest.mark.parametrize("topk", [513, 640, 641, 768, 1024])
 def test_rabitq_deferred_merge_iteration_limits(gpu, topk):
     """the deferred merge when the loop ends by max_iterations with keys still in the list
     (merged before the rerank), with K beyond one register, and on a graph smaller than the
@@ -362,9 +362,9 @@ def ragged_dataset(n, dim, degree, nq, seed):
 
 
 @pytest.mark.parametrize("dim", [64, 160])
-@pytest.mark.parametrize("topk", [768, 1024])
+@pytest.mark.parametrize("topk", [640, 768, 1024])
 def test_rabitq_deferred_merge_ragged_rows(gpu, dim, topk):
-    """beams of 12 and 16 registers at degree 256 (four candidate registers): a dense row's
+    """beams of 10, 12 and 16 registers at degree 256 (four candidate registers): a dense row's
     direct merge followed by a flush of 1-4 list keys.  The flush ranks its keys by the
     registers' last keys, which the direct merge must leave current; max_iterations that end
     the loop right after such a merge (the final flush) and full searches"""
