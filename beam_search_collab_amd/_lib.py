@@ -13,7 +13,8 @@ import os
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 HIP_LIB_PATH = os.path.join(_HERE, "libbs_hip.so")
-HOST_LIB_PATH = os.path.join(_HERE, "libbs_host.so")
+# BS_HOST_LIB names another build of the host library (the sanitizer build: make sanitize-check)
+HOST_LIB_PATH = os.environ.get("BS_HOST_LIB") or os.path.join(_HERE, "libbs_host.so")
 
 u32, u64, i32, f32, f64 = C.c_uint32, C.c_uint64, C.c_int32, C.c_float, C.c_double
 vp = C.c_void_p

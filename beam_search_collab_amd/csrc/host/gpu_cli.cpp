@@ -13,6 +13,7 @@
 // Exit status 1 on a configuration or input error, with the message on stderr.
 #include "bs_hip.h"
 #include "bs_host.h"
+#include "cli_config.hpp"
 #include "json_lite.hpp"
 
 #include <cstdint>
@@ -46,16 +47,11 @@ int main() {
         return die(std::string("JSON parse error: ") + e.what());
     }
     try {
-        if (j.has("search") && j.at("search").has("mode")) {
-            const std::string mode = j.at("search").at("mode").as_string();
-            if (mode.rfind("sophia_", 0) == 0)
-                return die("mode " + mode + ": the legacy sophia_* stack is not part of this build");
-        }
-        if (!j.has("data")) return die("Missing \"data\" key");
-        const jsonl::Value& jd = j.at("data");
-        const std::string graph_file = jd.at("graph").as_string(), base_file = jd.at("base").as_string(),
-                          query_file = jd.at("query").as_string(), gt_file = jd.at("gt").as_string(),
-                          codebook_file = jd.value("codebook", std::string());
+        cli::DataFiles files;
+        std::string err = cli::read_data(j, files);
+        if (!err.empty()) return die(err);
+        const std::string &graph_file = files.graph, &base_file = files.base, &query_file = files.query,
+                          &gt_file = files.gt, &codebook_file = files.codebook;
 
         Buf eb, vb, qb, gb;
         uint64_t n = 0, nv = 0, nq = 0, ngt = 0;
@@ -81,23 +77,15 @@ int main() {
         std::cout << "data: " << n << " points, dim=" << dim << ", degree=" << degree << ", queries=" << nq
                   << ", entry=" << entry << std::endl;
 
-        if (!j.has("search")) return die("Missing \"search\" key");
-        const jsonl::Value& js = j.at("search");
-        const std::string mode = js.value("mode", std::string("base"));
-        const int K = static_cast<int>(js.value("K", 100.0));
+        cli::SearchSettings ss;
+        if (!(err = cli::read_search_head(j, ss)).empty()) return die(err);
+        const std::string& mode = ss.mode;
+        const int K = ss.K;
         std::cout << "search: mode=" << mode << " K=" << K << std::endl;
-        if (K <= 0) return die("K must be positive");
-
-        bs_search_cfg cfg{};
-        cfg.K = static_cast<uint32_t>(K);
-        cfg.topk_size = static_cast<uint32_t>(js.value("topk_size", 256.0));
-        cfg.filter_capacity = static_cast<uint32_t>(js.value("filter_capacity", 1024.0));
-        cfg.max_iterations = static_cast<int32_t>(js.value("max_iterations", 1024.0));
-        cfg.reset_interval = static_cast<int32_t>(js.value("reset_interval", 16.0));
+        if (!(err = cli::read_search_rest(j, !codebook_file.empty(), ss)).empty()) return die(err);
+        bs_search_cfg cfg = ss.cfg;
         cfg.entry_point = entry;
-        cfg.queries_per_group = 1;
-        if (mode == "rabitq") {
-            if (codebook_file.empty()) return die("rabitq mode requires \"codebook\" in data config");
+        if (cfg.mode == BS_RABITQ) {
             uint32_t cb_entry = 0, pdim = 0;
             Buf cb, fb, sb;
             if (bs_read_codebook(codebook_file.c_str(), n, dim, degree, &cb_entry,
@@ -109,23 +97,7 @@ int main() {
             if (bs_index_attach_rabitq(ix, static_cast<uint32_t*>(cb.p), static_cast<float*>(fb.p),
                                        static_cast<float*>(sb.p), pdim))
                 return die(bs_last_error());
-            cfg.mode = BS_RABITQ;
             cfg.entry_point = (cb_entry != 0xFFFFFFFFu) ? cb_entry : entry;
-            cfg.reset_interval = 0;
-        } else {
-            if (cfg.topk_size < static_cast<uint32_t>(K))
-                return die("topk_size (" + std::to_string(cfg.topk_size) + ") must be >= K (" + std::to_string(K) + ")");
-            if (mode == "base") {
-                cfg.mode = BS_BASE;
-            } else if (mode.size() >= 5 && (mode.rfind("warp", 0) == 0 || mode.rfind("bwarp", 0) == 0)) {
-                const bool bloom = mode[0] == 'b';
-                const std::string ny = mode.substr(bloom ? 5 : 4);
-                if (ny != "1" && ny != "2" && ny != "4" && ny != "8") return die("Unknown mode: " + mode);
-                cfg.mode = bloom ? BS_GROUP_BLOOM : BS_GROUP;
-                cfg.queries_per_group = static_cast<uint32_t>(std::atoi(ny.c_str()));
-            } else {
-                return die("Unknown mode: " + mode);
-            }
         }
 
         const float* queries = static_cast<const float*>(qb.p);

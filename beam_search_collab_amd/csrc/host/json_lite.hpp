@@ -1,6 +1,7 @@
 // Minimal JSON reader for the CLI configs: objects, arrays, strings, numbers, true /
 // false / null, with // and /* */ comments (the reference parses its stdin config with
-// comments allowed, src/gpu_cli.cu:357).  Throws std::runtime_error on malformed input.
+// comments allowed, src/gpu_cli.cu:357).  Throws std::runtime_error on malformed input,
+// including arrays and objects nested more than 256 deep (each level is a recursion).
 #pragma once
 #include <cctype>
 #include <cstdlib>
@@ -52,6 +53,15 @@ public:
 private:
     const std::string& s_;
     size_t i_ = 0;
+    int depth_ = 0;
+    static constexpr int MAX_DEPTH = 256;
+    struct Nest {  // one level of array / object nesting, for the depth limit
+        Parser& p;
+        explicit Nest(Parser& q) : p(q) {
+            if (++p.depth_ > MAX_DEPTH) p.err("nesting deeper than 256 levels");
+        }
+        ~Nest() { --p.depth_; }
+    };
 
     [[noreturn]] void err(const std::string& m) {
         throw std::runtime_error("JSON parse error at offset " + std::to_string(i_) + ": " + m);
@@ -76,6 +86,7 @@ private:
         const char c = s_[i_];
         Value v;
         if (c == '{') {
+            Nest nest(*this);
             v.kind = Value::Object;
             ++i_;
             ws();
@@ -104,6 +115,7 @@ private:
             }
         }
         if (c == '[') {
+            Nest nest(*this);
             v.kind = Value::Array;
             ++i_;
             ws();

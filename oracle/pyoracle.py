@@ -11,7 +11,8 @@ import os
 import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "bin", "libbs_oracle.so")
+# BS_ORACLE_LIB / BS_ORACLE_MUTANT_LIB name other builds (the sanitizer build: make sanitize-check)
+LIB_PATH = os.environ.get("BS_ORACLE_LIB") or os.path.join(HERE, "bin", "libbs_oracle.so")
 REF_DIR = os.path.join(HERE, "_ref")
 
 BASE_HASH, BASE_BLOOM, RABITQ_GPU, BASE_CPUREF, RABITQ_CPUREF = 0, 1, 2, 3, 4
@@ -74,7 +75,7 @@ def lib():
     return _lib
 
 
-MUTANT_PATH = os.path.join(HERE, "bin", "libbs_oracle_mutant.so")
+MUTANT_PATH = os.environ.get("BS_ORACLE_MUTANT_LIB") or os.path.join(HERE, "bin", "libbs_oracle_mutant.so")
 MUTANT_SEEN_AT_ENTRY, MUTANT_REEXPAND, MUTANT_NO_DEDUP = 1, 2, 3
 _mlib = None
 
