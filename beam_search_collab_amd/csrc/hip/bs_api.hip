@@ -131,6 +131,8 @@ void make_pivots(const float* vecs, uint64_t n, uint32_t dim, std::vector<float>
         pnorm[t] = static_cast<float>(nn);
     }
 }
+// the device address of bs_search_device_noalloc's static workspace (defined below)
+int noalloc_workspace(int dev, uint32_t** out);
 }  // namespace
 
 extern "C" const char* bs_last_error(void) { return g_err.c_str(); }
@@ -181,6 +183,13 @@ extern "C" int bs_index_create(const float* vecs, const uint32_t* edges, uint64_
     if (rc) return rc;
     int device = 0;
     HIP_TRY(hipGetDevice(&device));
+    {
+        // bs_search_device_noalloc's workspace address on this device, looked up here, at
+        // set-up, so that no later call (one under graph capture, say) makes the lookup
+        uint32_t* ws = nullptr;
+        rc = noalloc_workspace(device, &ws);
+        if (rc) return rc;
+    }
     bs_index_s* ix = new bs_index_s();
     ix->n = n;
     ix->dim = dim;
@@ -727,6 +736,7 @@ std::mutex g_scratch_mutex;
 uint32_t* g_scratch_ptr[MAX_DEVICES] = {};
 
 // this device's address of `scratch`, looked up once per device with that device current
+// (bs_index_create makes the first lookup for its device)
 int noalloc_workspace(int dev, uint32_t** out) {
     if (dev < 0 || dev >= MAX_DEVICES) return fail(BS_EINVAL, "device ordinal out of range");
     std::lock_guard<std::mutex> lock(g_scratch_mutex);

@@ -124,7 +124,11 @@ int bs_search_device(bs_index idx, const bs_search_cfg* cfg, const float* d_quer
  * 262144 queries per call (the workspace's size; larger nq is rejected with BS_EINVAL).
  * Asynchronous on `stream`; buffers as for bs_search_device.  Every call on one GPU shares
  * the array: calls that overlap on one GPU (other streams, other threads) race; calls in
- * order on one stream do not.  The current device must be the index's. */
+ * order on one stream do not.  The current device must be the index's.  A call may be
+ * recorded into a HIP graph (stream capture) and replayed: it issues kernel launches only
+ * (the array's address is looked up once per device by bs_index_create, and the bucket
+ * counters are cleared by a kernel, not a memset); tested with three replays of a captured
+ * scheduled call against bs_search_device. */
 int bs_search_device_noalloc(bs_index idx, const bs_search_cfg* cfg, const float* d_queries,
                              uint64_t nq, uint32_t* d_results, float* d_dists,
                              uint32_t* d_per_query, void* stream);

@@ -64,3 +64,47 @@ def test_noalloc_rejects_more_queries_than_its_workspace(gpu):
     res = torch.empty((nq, 10), dtype=torch.int32, device=dev)
     with pytest.raises(ValueError, match="static workspace"):
         g.search_device_noalloc(q_t.data_ptr(), nq, res.data_ptr(), 10, "base", GPUBaseSearchCfg(64, 1024, entry))
+
+
+def test_noalloc_under_graph_capture(gpu):
+    """one bs_search_device_noalloc call recorded into a HIP graph on a side stream (query
+    scheduling on: labels, bucket sort and the search, with the histogram cleared by a kernel),
+    replayed three times with eager work and synchronizations in between (an eager scheduled
+    call on other queries, which leaves its own contents in the shared workspace): every replay
+    gives the ids, distances and per-query counters of bs_search_device"""
+    import torch
+    g, entry, erq = _index()
+    dev = torch.device("cuda:0")
+    q_t = torch.from_numpy(host.gen_mixture(5000, 64, 16, 0.0, 128.0, 12.0, 0.0, 41, 44)).to(dev)
+    # other queries, also scheduled (>= 4096): between replays they overwrite the static workspace
+    q_other = torch.from_numpy(host.gen_mixture(4500, 64, 16, 0.0, 128.0, 12.0, 0.0, 41, 45)).to(dev)
+    nq, K = q_t.shape[0], 10
+    for mode in ("base", "rabitq"):
+        cfg = (GPURabitqSearchCfg(128, 1024, erq, 1024) if mode == "rabitq"
+               else GPUBaseSearchCfg(128, 1024, entry, 1024, 16))
+        want = _run(g, g.search_device, q_t, K, mode, cfg)
+        res = torch.full((nq, K), -7, dtype=torch.int32, device=dev)
+        dist = torch.full((nq, K), -1.0, dtype=torch.float32, device=dev)
+        pq = torch.zeros((nq, 5), dtype=torch.int32, device=dev)
+        side = torch.cuda.Stream()
+        graph = torch.cuda.CUDAGraph()
+        torch.cuda.synchronize()
+        with torch.cuda.graph(graph, stream=side):
+            g.search_device_noalloc(q_t.data_ptr(), nq, res.data_ptr(), K, mode, cfg, d_dists=dist.data_ptr(),
+                                    d_per_query=pq.data_ptr(), stream=side.cuda_stream)
+        torch.cuda.synchronize()
+        for rep in range(3):
+            res.fill_(-7)
+            dist.fill_(-1.0)
+            pq.zero_()
+            other = _run(g, g.search_device_noalloc, q_other, K, mode, cfg)  # eager work between
+            assert (other[0] != -7).all()
+            torch.cuda.synchronize()
+            graph.replay()
+            torch.cuda.synchronize()
+            got = (res.cpu().numpy(), dist.cpu().numpy(), pq.cpu().numpy())
+            ctx = (mode, rep)
+            assert np.array_equal(got[0], want[0]), ctx
+            assert got[1].tobytes() == want[1].tobytes(), ctx
+            assert np.array_equal(got[2], want[2]), ctx
+        del graph
