@@ -2,6 +2,7 @@
 // inputs so the parity tests can check each block against the CPU oracle.
 #include "bs_hip.h"
 #include "bs_device.hpp"
+#include "bs_order.hpp"
 
 #include <hip/hip_runtime.h>
 
@@ -324,6 +325,37 @@ extern "C" int bs_debug_sort(const uint64_t* keys, uint32_t n, uint64_t* out) tr
     else hipLaunchKernelGGL(dbg_sort_kernel<16>, dim3(1), dim3(64), 0, nullptr, dk.p, n, dout.p);
     DTRY(hipGetLastError());
     DTRY(hipMemcpy(out, dout.p, n * 8, hipMemcpyDeviceToHost));
+    return BS_OK;
+} catch (...) {
+    return bs_internal_exception();
+}
+
+// ---------------------------------------------------------------------------
+// cost order of the RaBitQ query scheduling
+// ---------------------------------------------------------------------------
+extern "C" int bs_debug_cost_order(const float* signal, uint64_t n, uint32_t* qmap, uint32_t* bucket) try {
+    if (n == 0) return BS_OK;
+    if (n > (1u << 18)) return dfail(BS_EINVAL, "n must be <= 262144");
+    DevBuf<uint32_t> key, map, hist, cursor;
+    DTRY(key.alloc(n));
+    DTRY(map.alloc(n));
+    DTRY(hist.alloc(bso::ORDER_P));
+    DTRY(cursor.alloc(bso::ORDER_P));
+    DTRY(hipMemcpy(key.p, signal, n * 4, hipMemcpyHostToDevice));
+    DTRY(hipMemset(hist.p, 0, bso::ORDER_P * 4));
+    DTRY(hipMemset(map.p, 0xFF, n * 4));
+    bso::OrderParams o;
+    std::memset(&o, 0, sizeof(o));
+    o.nq = n;
+    o.key = key.p;
+    o.qmap = map.p;
+    o.hist = hist.p;
+    o.cursor = cursor.p;
+    o.g = 1;
+    o.X = 1;
+    DTRY(bso::launch_cost_order(o, nullptr));
+    DTRY(hipMemcpy(qmap, map.p, n * 4, hipMemcpyDeviceToHost));
+    DTRY(hipMemcpy(bucket, key.p, n * 4, hipMemcpyDeviceToHost));
     return BS_OK;
 } catch (...) {
     return bs_internal_exception();

@@ -114,6 +114,90 @@ __global__ void __launch_bounds__(256) order_place(const OrderParams o) {
     if (pos < o.nq) o.qmap[pos] = static_cast<uint32_t>(q);
 }
 
+// Cost order.  A launch of several rounds of queries ends when its last-started queries do,
+// so the queries expected to run longest go first.  key[q] holds the signal as a float;
+// the 256 buckets span mean +- 2 standard deviations of the finite signals, taken over
+// those within 3 standard deviations of the mean of all of them (so that a few far values
+// do not squeeze the rest into a few buckets); bucket 0 = largest.
+// One workgroup: the range, kept in cursor[0..1] as float bits until order_scan.
+__device__ __forceinline__ void cost_moments(const OrderParams& o, double clo, double chi, double* s1, double* s2,
+                                             double* sn, double& mu, double& sd) {
+    const uint32_t t = threadIdx.x;
+    double a = 0.0, b = 0.0, n = 0.0;
+    for (uint64_t q = t; q < o.nq; q += 256) {
+        const double d = __uint_as_float(o.key[q]);
+        if (d >= clo && d <= chi) {  // false for NaN
+            a += d;
+            b += d * d;
+            n += 1.0;
+        }
+    }
+    s1[t] = a;
+    s2[t] = b;
+    sn[t] = n;
+    __syncthreads();
+    for (uint32_t h = 128; h > 0; h >>= 1) {
+        if (t < h) {
+            s1[t] += s1[t + h];
+            s2[t] += s2[t + h];
+            sn[t] += sn[t + h];
+        }
+        __syncthreads();
+    }
+    mu = sn[0] > 0.0 ? s1[0] / sn[0] : 0.0;
+    const double var = sn[0] > 0.0 ? s2[0] / sn[0] - mu * mu : 0.0;
+    sd = var > 0.0 ? sqrt(var) : 0.0;
+    __syncthreads();
+}
+
+__global__ void __launch_bounds__(256) cost_range(const OrderParams o) {
+    __shared__ double s1[256], s2[256], sn[256];
+    const double fmax = 3.4028234663852886e38;
+    double mu, sd;
+    cost_moments(o, -fmax, fmax, s1, s2, sn, mu, sd);
+    cost_moments(o, mu - 3.0 * sd, mu + 3.0 * sd, s1, s2, sn, mu, sd);
+    if (threadIdx.x == 0) {
+        float lo = static_cast<float>(mu - 2.0 * sd), hi = static_cast<float>(mu + 2.0 * sd);
+        if (!(hi > lo)) hi = lo + 1.0f;
+        o.cursor[0] = __float_as_uint(lo);
+        o.cursor[1] = __float_as_uint(hi);
+    }
+}
+
+// Thread per query: its bucket (in place of the signal) and the bucket counts.
+__global__ void __launch_bounds__(256) cost_key(const OrderParams o) {
+    const uint64_t q = static_cast<uint64_t>(blockIdx.x) * 256 + threadIdx.x;
+    if (q >= o.nq) return;
+    const float lo = __uint_as_float(o.cursor[0]), hi = __uint_as_float(o.cursor[1]);
+    const float d = __uint_as_float(o.key[q]);
+    uint32_t b = 0;  // above the range, infinite or NaN: first
+    if (d <= lo) {
+        b = ORDER_P - 1;
+    } else if (d < hi) {
+        const float f = (hi - d) / (hi - lo) * static_cast<float>(ORDER_P);
+        b = f >= static_cast<float>(ORDER_P - 1) ? ORDER_P - 1 : f >= 0.0f ? static_cast<uint32_t>(f) : 0u;
+    }
+    o.key[q] = b;
+    atomicAdd(&o.hist[b], 1u);
+}
+
+hipError_t launch_cost_order(const OrderParams& o, hipStream_t s) {
+    OrderParams c = o;
+    c.X = 1;
+    c.start[0] = 0;
+    hipLaunchKernelGGL(cost_range, dim3(1), dim3(256), 0, s, c);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(cost_key, dim3(static_cast<uint32_t>((c.nq + 255) / 256)), dim3(256), 0, s, c);
+    e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(order_scan, dim3(1), dim3(ORDER_P), 0, s, c);
+    e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(order_place, dim3(static_cast<uint32_t>((c.nq + 255) / 256)), dim3(256), 0, s, c);
+    return hipGetLastError();
+}
+
 hipError_t launch_order(const OrderParams& o, hipStream_t s) {
     hipLaunchKernelGGL(order_key, dim3(static_cast<uint32_t>((o.nq + 31) / 32)), dim3(256), 0, s, o);
     hipError_t e = hipGetLastError();

@@ -26,4 +26,9 @@ struct OrderParams {
 // order_key, order_scan, order_place on stream s (nq >= 1)
 hipError_t launch_order(const OrderParams& o, hipStream_t s);
 
+// Launch map by predicted cost, longest first (nq >= 1): on entry key[q] holds query q's
+// cost signal as a float (larger = longer); cost_range, cost_key, order_scan and
+// order_place with one run (o.X and o.start are ignored); cursor[0..1] is scratch.
+hipError_t launch_cost_order(const OrderParams& o, hipStream_t s);
+
 }  // namespace bso

@@ -287,6 +287,16 @@ def debug_sort(keys):
     return out
 
 
+def debug_cost_order(signal):
+    """(qmap, bucket) of the RaBitQ launch order for per-query cost signals (bs_debug_cost_order)"""
+    signal = np.ascontiguousarray(signal, dtype=np.float32)
+    n = signal.shape[0]
+    qmap = np.empty(n, np.uint32)
+    bucket = np.empty(n, np.uint32)
+    _check(_lib.hip().bs_debug_cost_order(_ptr(signal), n, _ptr(qmap), _ptr(bucket)), "bs_debug_cost_order")
+    return qmap, bucket
+
+
 def debug_mfma32(A, B):
     A = np.ascontiguousarray(A, dtype=np.float32).reshape(32, 2)
     B = np.ascontiguousarray(B, dtype=np.float32).reshape(2, 32)

@@ -135,11 +135,15 @@ int bs_search_device_noalloc(bs_index idx, const bs_search_cfg* cfg, const float
 
 /* Query scheduling (no counterpart in the reference, whose launches run query i in
  * block i, src/gpu_cli.cu:94-95,111-112,128-129).  Queries are independent, so their order
- * changes no result; it changes where their gathers hit.  With scheduling on, a search
- * launch first labels each query with its nearest of 256 pivot rows (fixed at
- * bs_index_create), sorts the queries by label and gives each XCD a contiguous run of
- * them, so queries that walk the same region share that XCD's L2.  Results, distances and
- * per-query counters are written at each query's own row as before.  mode 0: off;
+ * changes no result; it changes where their gathers hit and when the launch ends.  With
+ * scheduling on, a base / warp / bwarp launch first labels each query with its nearest of
+ * 256 pivot rows (fixed at bs_index_create), sorts the queries by label and gives each XCD
+ * a contiguous run of them, so queries that walk the same region share that XCD's L2.  A
+ * RaBitQ launch is ordered longest first by predicted cost instead: a pilot search (topk
+ * 16, 24 iterations, K 1) gives each query the exact distance of the best row it reaches,
+ * and the queries run in descending order of it (the launch of several rounds then ends
+ * with short queries).  Results, distances and per-query counters are written at each
+ * query's own row as before.  mode 0: off;
  * 1 (default): on for calls with nq >= 4096; 2: on for every call.  Scheduled calls run
  * in launches of at most 262144 queries and share a workspace of the index; a call made
  * on another stream waits for the previous scheduled call on the device. */
@@ -230,6 +234,14 @@ int bs_debug_beam(uint32_t topk, const uint64_t* keys, uint32_t nbatch, uint32_t
 /* Full sort of n (<= 1024) keys ascending (the rerank sorter; replaces the bitonic
  * re-sort of topk_shared.cuh:384-416). */
 int bs_debug_sort(const uint64_t* keys, uint32_t n, uint64_t* out);
+
+/* The cost order of RaBitQ query scheduling on n (<= 262144) signals (host f32, larger =
+ * expected to run longer): qmap[p] = the query at launch position p (longest first), bucket[q]
+ * = query q's bucket (0 = largest; 256 buckets over mean +- 2 standard deviations of the
+ * finite signals within 3 standard deviations of the mean of all finite signals; NaN and
+ * values above the range in bucket 0, values below it in bucket 255).  No counterpart in the
+ * reference (its launches run query i in block i). */
+int bs_debug_cost_order(const float* signal, uint64_t n, uint32_t* qmap, uint32_t* bucket);
 
 /* One v_mfma_f32_32x32x2f32 product: A 32x2 and B 2x32 row-major in, D = A B 32x32
  * row-major out, read back through the accumulator layout the ground-truth kernel uses. */

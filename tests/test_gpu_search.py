@@ -118,7 +118,7 @@ def test_base_waves_per_query(gpu, nq):
         assert np.array_equal(ids_w, ids_b)
 
 
-@pytest.mark.parametrize("nq", [1, 5, 9, 63, 257, 1000])
+@pytest.mark.parametrize("nq", [1, 5, 9, 63, 257, 1000, 5000])
 def test_query_order_changes_no_result(gpu, nq):
     """query scheduling (labels, bucket sort, a run of queries per XCD) only permutes which
     launch slot runs which query: ids, distances and counters per query are unchanged,
@@ -407,3 +407,28 @@ def test_rabitq_trees_match_reference_cpu_cli(gpu, name):
         assert np.array_equal(ids, arrays[s["key"]]), (name, s)
         assert d.tobytes() == arrays["dists_" + s["key"][4:]].tobytes(), (name, s)
         assert abs(st["expansions"] / arrays["queries"].shape[0] - s["expansions_per_query"]) < 1e-9
+
+
+def test_rabitq_cost_order(gpu):
+    """the RaBitQ launch order (bs_debug_cost_order): the launch map is a permutation that runs
+    larger signals first (buckets non-decreasing along the launch, a bucket never larger for a
+    larger signal), NaN and values far above the rest first, values far below last, a few far
+    values leave the bulk spread over many buckets, and a constant signal stays in one bucket"""
+    rng = np.random.default_rng(21)
+    for n in (1, 2, 255, 256, 257, 5000, 262144):
+        s = rng.gamma(4.0, 1000.0, n).astype(np.float32)
+        if n > 10:
+            s[:5] = [np.nan, np.inf, 1e30, -1e30, -np.inf]
+        qmap, b = search.debug_cost_order(s)
+        assert np.array_equal(np.sort(qmap), np.arange(n)), n
+        assert (np.diff(b[qmap].astype(np.int64)) >= 0).all(), n
+        assert b.max() <= 255
+        fin = np.isfinite(s)
+        o = np.argsort(s[fin], kind="stable")
+        assert (np.diff(b[fin][o].astype(np.int64)) <= 0).all(), n
+        if n > 10:
+            assert list(b[:5]) == [0, 0, 0, 255, 255], (n, b[:5])
+        if n >= 5000:
+            assert len(np.unique(b)) > 200, n
+    qmap, b = search.debug_cost_order(np.full(1000, 7.0, np.float32))
+    assert np.array_equal(np.sort(qmap), np.arange(1000)) and len(np.unique(b)) == 1
