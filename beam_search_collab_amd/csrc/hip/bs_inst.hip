@@ -81,6 +81,18 @@ hipError_t launch_search_rabitq(const SearchParams& p, int TR, int CR, int PB, d
                               hipStream_t s, int* occ) {
     return launch_any(p, TR, CR, PB, g, b, lds, s, occ);
 }
+#ifdef BS_PHASE_CLOCKS
+// the instrumented library's clock sums of the narrow-code RaBitQ instances (PhaseClock):
+// out[0..16) as bs_phase_clock holds them; reset != 0 clears them afterwards
+extern "C" int bs_phase_read(unsigned long long* out, int reset) {
+    if (hipMemcpyFromSymbol(out, HIP_SYMBOL(bs_phase_clock), sizeof(unsigned long long) * 16) != hipSuccess) return 1;
+    if (reset) {
+        const unsigned long long z[16] = {};
+        if (hipMemcpyToSymbol(HIP_SYMBOL(bs_phase_clock), z, sizeof(z)) != hipSuccess) return 2;
+    }
+    return 0;
+}
+#endif
 #else
 hipError_t launch_search_rabitq_wide(const SearchParams& p, int TR, int CR, int PB, dim3 g, dim3 b, size_t lds,
                               hipStream_t s, int* occ) {

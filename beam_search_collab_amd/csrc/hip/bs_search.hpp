@@ -42,6 +42,37 @@ struct SearchParams {
     L2Shape L;
 };
 
+// Per-phase clocks of the RaBitQ loop, compiled only into the instrumented library (make
+// phase: -DBS_PHASE_CLOCKS, libbs_hip_phase.so, read by bs_phase_read): s_memtime at the
+// phase boundaries, summed per query and added to bs_phase_clock at the query's end (slots
+// 0-5 the loop's phases, 6 the final flush, rerank and results, 8 expansions, 9 iterations,
+// 10 queries).  In the library itself every call below is empty.
+#ifdef BS_PHASE_CLOCKS
+static __device__ unsigned long long bs_phase_clock[16];
+#endif
+struct PhaseClock {
+#ifdef BS_PHASE_CLOCKS
+    uint64_t t = 0, acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    __device__ __forceinline__ void start() { t = __builtin_amdgcn_s_memtime(); }
+    __device__ __forceinline__ void mark(int i) {
+        const uint64_t n = __builtin_amdgcn_s_memtime();
+        acc[i] += n - t;
+        t = n;
+    }
+    __device__ __forceinline__ void flush(uint32_t n_exp, uint32_t n_iter) {
+        if (lane_id() != 0) return;
+        for (int i = 0; i < 8; ++i) atomicAdd(&bs_phase_clock[i], static_cast<unsigned long long>(acc[i]));
+        atomicAdd(&bs_phase_clock[8], static_cast<unsigned long long>(n_exp));
+        atomicAdd(&bs_phase_clock[9], static_cast<unsigned long long>(n_iter));
+        atomicAdd(&bs_phase_clock[10], 1ull);
+    }
+#else
+    __device__ __forceinline__ void start() {}
+    __device__ __forceinline__ void mark(int) {}
+    __device__ __forceinline__ void flush(uint32_t, uint32_t) {}
+#endif
+};
+
 // Register budget per instance, matched to what the LDS slice allows anyway: RaBitQ beams
 // up to 256 (about 7 KB of LDS per wavefront) are compiled for 5 wavefronts per SIMD (at most
 // 96 VGPRs); the loops with beams up to 256 and two passes of rows in flight (Bloom over rows
@@ -323,11 +354,14 @@ search_kernel(const SearchParams p) {
         // compaction and its read-back, when no merge runs)
         PendingList pd = {DEFER ? reinterpret_cast<uint64_t*>(my + p.off_pend) : nullptr, 0u, EMPTY_KEY};
         uint32_t picks = 0;
+        PhaseClock clk;
+        clk.start();
 
         for (int32_t iter = 0; iter < p.max_it; ++iter) {
             ++n_iter;
             const uint32_t parent = DEFER ? pending_pick<TR, true>(beam, st, pd, T, scratch, merge_aux, picks)
                                           : beam_pick<TR, true>(beam, st);
+            clk.mark(0);
             if (parent == INVALID) break;
             const uint32_t* rec = p.recs + static_cast<uint64_t>(parent) * rstride;
             const float* fac = reinterpret_cast<const float*>(rec + p.rec_fac);
@@ -368,7 +402,9 @@ search_kernel(const SearchParams p) {
             // The expanded set is probed while the record is in flight: the loads of a node
             // already expanded (gpu_search_rabitq.cuh:249-252; 7.5% of the picks at config C)
             // are wasted, the probe's LDS latency of every other pick is hidden.
-            if (!hf.insert1(parent)) continue;
+            const bool fresh_parent = hf.insert1(parent) != 0u;
+            clk.mark(1);
+            if (!fresh_parent) continue;
             ++n_exp;
 
             // exact distance of the parent
@@ -376,6 +412,7 @@ search_kernel(const SearchParams p) {
             l2_accum<QMAX, 1>(q, pv, lig, L, pe);
             const float exact = __uint_as_float(readlane(__float_as_uint(bsw::group_sum(pe[0], L.G)), 0));
             ++n_dist;
+            clk.mark(2);
             // fastscan sums of the neighbours
             uint32_t raw[CR];
             if constexpr (WIDE) {
@@ -394,6 +431,7 @@ search_kernel(const SearchParams p) {
 #pragma unroll
                 for (int rc = 0; rc < CR; ++rc) raw[rc] = raw_quad(pl, cw[rc < NC ? rc : 0]);
             }
+            clk.mark(3);
             // Only neighbours below the beam's last key can enter it (the merge drops the
             // others first), so only they are looked up in the expanded set.  The estimate
             // counter (neighbours not yet expanded: the reference's estimates) needs every
@@ -417,8 +455,10 @@ search_kernel(const SearchParams p) {
             }
             wave_sync();
             n_est += nv;
+            clk.mark(4);
             if constexpr (DEFER) pending_add<TR, CR>(beam, ck, cm, pd, T, scratch, merge_aux, st);
             else beam_merge<TR, CR>(beam, ck, cm, T, scratch, merge_aux, st);
+            clk.mark(5);
         }
         if constexpr (DEFER) pending_flush<TR>(beam, pd, T, scratch, merge_aux, st);
 
@@ -480,6 +520,8 @@ search_kernel(const SearchParams p) {
                 if (dout) dout[wpos[r]] = key_dist(beam[r]);
             }
         }
+        clk.mark(6);
+        clk.flush(n_exp, n_iter);
     }
 
     if (p.per_query && lane == 0) {
