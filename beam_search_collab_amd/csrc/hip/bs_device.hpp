@@ -298,32 +298,6 @@ __device__ __forceinline__ uint64_t beam_peek(const uint64_t (&beam)[TR], BeamSt
     return readlane64(row, pl);
 }
 
-// Mark the beam key kp found by beam_peek at slot `at`.  RUN: of a run of identical keys
-// the last one is marked, which keeps the beam sorted.
-template <int TR, bool RUN>
-__device__ __forceinline__ void beam_mark(uint64_t (&beam)[TR], BeamState& st, uint32_t at, uint64_t kp) {
-    const uint32_t pr = at >> 6, pl = at & 63u;
-    uint32_t qr = pr, ql = pl;
-    if constexpr (RUN) {
-        // identical keys are rare: look at the next element first, scan only if it repeats
-        uint64_t nxt = EMPTY_KEY;
-        if (pl < 63u) nxt = readlane64(beam_reg<TR>(beam, pr), pl + 1u);
-        else if (pr + 1u < static_cast<uint32_t>(TR)) nxt = readlane64(beam_reg<TR>(beam, pr + 1u), 0u);
-        if (nxt == kp) {
-#pragma unroll
-            for (int r = 0; r < TR; ++r) {
-                const uint64_t mm = ballot(beam[r] == kp);
-                if (static_cast<uint32_t>(r) >= pr && mm != 0) {
-                    qr = static_cast<uint32_t>(r);
-                    ql = 63u - static_cast<uint32_t>(__builtin_clzll(mm));
-                }
-            }
-        }
-    }
-    // set the mark (key LSB) of element (qr, ql)
-    beam[qr] |= bsw::lane_in(1ull << ql) ? 1ull : 0ull;
-}
-
 template <int TR, bool RUN>
 __device__ __forceinline__ uint32_t beam_pick(uint64_t (&beam)[TR], BeamState& st, uint64_t* next_key = nullptr) {
     // the first register holding an unexpanded key, its first such lane
@@ -527,15 +501,31 @@ __device__ __forceinline__ uint32_t pending_pick(uint64_t (&beam)[TR], BeamState
         if (below >= T) return INVALID;
     }
     ++picks;
+    // The slot to mark, (mr, ml), with ml = 64 for a pick from the list: one register-indexed
+    // write on every path.  A write on some paths only made the compiler copy the whole
+    // beam (its registers as one 32-register tuple) to another tuple and back at the join:
+    // 32 64-bit moves per mark at 10 registers.
+    uint32_t mr = 0, ml = 64;
     if (from_list) {
         const uint32_t l = static_cast<uint32_t>(__builtin_ctzll(ballot(v == u)));
         pd.v = v | (lane == l ? 1ull : 0ull);
-    } else if (RUN && kn == u) {
-        beam_mark<TR, true>(beam, st, at, ub);
     } else {
-        // u is the last of its run: mark it in place
-        beam_mark<TR, false>(beam, st, at, ub);
+        mr = at >> 6;
+        ml = at & 63u;
+        if (RUN && kn == u) {
+            // of a run of identical keys the last one is marked (the beam stays sorted)
+#pragma unroll
+            for (int r = 0; r < TR; ++r) {
+                const uint64_t mm = ballot(beam[r] == ub);
+                if (static_cast<uint32_t>(r) >= (at >> 6) && mm != 0) {
+                    mr = static_cast<uint32_t>(r);
+                    ml = 63u - static_cast<uint32_t>(__builtin_clzll(mm));
+                }
+            }
+        }
     }
+    const uint64_t lm = ml < 64u ? (1ull << ml) : 0ull;
+    beam[mr] |= bsw::lane_in(lm) ? 1ull : 0ull;
     return key_id(u);
 }
 
