@@ -570,9 +570,10 @@ hipError_t launch(const Plan& pl, hipStream_t s) {
 // 1024) and a launch of several rounds ends with its last-started long queries; locality
 // gains nothing there (labels 5.65 ms, query order 5.44, measured costs longest-first 4.43).
 // The signal is the exact distance of the best row a short search finds (PILOT_T keys,
-// PILOT_IT iterations): Spearman +0.74 with the full search's iterations at config C.
-// Launch with pilot and cost order 4.74 ms (pilot 0.14 ms).
-constexpr uint32_t PILOT_T = 16, PILOT_IT = 24, PILOT_CAP = 64;
+// PILOT_IT iterations): Spearman +0.61 with the full search's iterations at config C (+0.74
+// with 24 iterations, which order the launch no better: 4.64 ms either way; pilot 0.087 ms
+// against 0.139).
+constexpr uint32_t PILOT_T = 16, PILOT_IT = 12, PILOT_CAP = 64;
 
 // The pilot search of one chunk: K = 1, distances into key[0..m) as floats (the cost order
 // reads them there), ids into qmap[0..m) (overwritten by the launch map).

@@ -27,8 +27,9 @@ struct OrderParams {
 hipError_t launch_order(const OrderParams& o, hipStream_t s);
 
 // Launch map by predicted cost, longest first (nq >= 1): on entry key[q] holds query q's
-// cost signal as a float (larger = longer); cost_range, cost_key, order_scan and
-// order_place with one run (o.X and o.start are ignored); cursor[0..1] is scratch.
+// cost signal as a float (larger = longer), on return its bucket; o.X and o.start are
+// ignored (one run).  Up to 65536 queries one workgroup does it all (cost_order_one);
+// above, cost_range, cost_key, order_scan and order_place, with cursor[0..1] as scratch.
 hipError_t launch_cost_order(const OrderParams& o, hipStream_t s);
 
 }  // namespace bso
