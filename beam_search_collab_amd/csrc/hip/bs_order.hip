@@ -18,6 +18,10 @@ namespace bso {
 
 using namespace bsw;
 
+// launches of up to ONE_WG queries are ordered in one workgroup after the labels (order_one,
+// cost_order_one): LDS counts and placement instead of global atomics and more launches
+constexpr uint64_t ONE_WG = 65536;
+
 __device__ __forceinline__ uint32_t orderable(float f) {
     const uint32_t b = __float_as_uint(f);
     return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
@@ -79,7 +83,7 @@ __global__ void __launch_bounds__(256) order_key(const OrderParams o) {
         for (int v = 1; v < 4; ++v) b = best_s[v][lane] < b ? best_s[v][lane] : b;
         const uint32_t label = static_cast<uint32_t>(b) & (ORDER_P - 1);
         o.key[q0 + lane] = label;
-        atomicAdd(&o.hist[label], 1u);
+        if (o.nq > ONE_WG) atomicAdd(&o.hist[label], 1u);  // below, order_one counts in LDS
     }
 }
 
@@ -101,16 +105,21 @@ __global__ void __launch_bounds__(ORDER_P) order_scan(const OrderParams o) {
     o.hist[t] = 0u;
 }
 
-// Thread per query: its rank in label order, then its launch position.
-__global__ void __launch_bounds__(256) order_place(const OrderParams o) {
-    const uint64_t q = static_cast<uint64_t>(blockIdx.x) * 256 + threadIdx.x;
-    if (q >= o.nq) return;
-    const uint32_t r = atomicAdd(&o.cursor[o.key[q]], 1u);
+// launch position of the query of label-order rank r: XCD x's run starts at rank start[x];
+// XCD x runs workgroups x, x + X, ... of g queries each
+__device__ __forceinline__ uint64_t order_pos(const OrderParams& o, uint32_t r) {
     uint32_t x = 0;
     while (x + 1 < o.X && o.start[x + 1] <= r) ++x;
     const uint32_t j = r - o.start[x];
     const uint64_t b = x + static_cast<uint64_t>(o.X) * (j / o.g);
-    const uint64_t pos = b * o.g + j % o.g;
+    return b * o.g + j % o.g;
+}
+
+// Thread per query: its rank in label order, then its launch position.
+__global__ void __launch_bounds__(256) order_place(const OrderParams o) {
+    const uint64_t q = static_cast<uint64_t>(blockIdx.x) * 256 + threadIdx.x;
+    if (q >= o.nq) return;
+    const uint64_t pos = order_pos(o, atomicAdd(&o.cursor[o.key[q]], 1u));
     if (pos < o.nq) o.qmap[pos] = static_cast<uint32_t>(q);
 }
 
@@ -195,10 +204,9 @@ __global__ void __launch_bounds__(256) cost_key(const OrderParams o) {
     atomicAdd(&o.hist[b], 1u);
 }
 
-// The whole cost order in one workgroup, for launches of up to COST_ONE_WG queries: range,
+// The whole cost order in one workgroup, for launches of up to ONE_WG queries: range,
 // buckets and counts in LDS, the scan, the placement (4 launches and their global atomics
 // took 0.07 ms at 10k queries).  Leaves hist and cursor untouched.
-constexpr uint64_t COST_ONE_WG = 65536;
 __global__ void __launch_bounds__(1024) cost_order_one(const OrderParams o) {
     __shared__ double s1[1024], s2[1024], sn[1024];
     __shared__ uint32_t cnt[ORDER_P], cur[ORDER_P];
@@ -228,7 +236,7 @@ hipError_t launch_cost_order(const OrderParams& o, hipStream_t s) {
     OrderParams c = o;
     c.X = 1;
     c.start[0] = 0;
-    if (c.nq <= COST_ONE_WG) {
+    if (c.nq <= ONE_WG) {
         hipLaunchKernelGGL(cost_order_one, dim3(1), dim3(1024), 0, s, c);
         return hipGetLastError();
     }
@@ -245,10 +253,37 @@ hipError_t launch_cost_order(const OrderParams& o, hipStream_t s) {
     return hipGetLastError();
 }
 
+// order_scan and order_place in one workgroup, with the label counts in LDS (launches of up to
+// ONE_WG queries; order_key then leaves hist alone)
+__global__ void __launch_bounds__(1024) order_one(const OrderParams o) {
+    __shared__ uint32_t cnt[ORDER_P], cur[ORDER_P];
+    const uint32_t t = threadIdx.x;
+    if (t < ORDER_P) cnt[t] = 0u;
+    __syncthreads();
+    for (uint64_t q = t; q < o.nq; q += 1024) atomicAdd(&cnt[o.key[q]], 1u);
+    __syncthreads();
+    if (t == 0) {
+        uint32_t a = 0;
+        for (uint32_t b = 0; b < ORDER_P; ++b) {
+            cur[b] = a;
+            a += cnt[b];
+        }
+    }
+    __syncthreads();
+    for (uint64_t q = t; q < o.nq; q += 1024) {
+        const uint64_t pos = order_pos(o, atomicAdd(&cur[o.key[q]], 1u));
+        if (pos < o.nq) o.qmap[pos] = static_cast<uint32_t>(q);
+    }
+}
+
 hipError_t launch_order(const OrderParams& o, hipStream_t s) {
     hipLaunchKernelGGL(order_key, dim3(static_cast<uint32_t>((o.nq + 31) / 32)), dim3(256), 0, s, o);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
+    if (o.nq <= ONE_WG) {
+        hipLaunchKernelGGL(order_one, dim3(1), dim3(1024), 0, s, o);
+        return hipGetLastError();
+    }
     hipLaunchKernelGGL(order_scan, dim3(1), dim3(ORDER_P), 0, s, o);
     e = hipGetLastError();
     if (e != hipSuccess) return e;
