@@ -140,7 +140,7 @@ int bs_search_device_noalloc(bs_index idx, const bs_search_cfg* cfg, const float
  * 256 pivot rows (fixed at bs_index_create), sorts the queries by label and gives each XCD
  * a contiguous run of them, so queries that walk the same region share that XCD's L2.  A
  * RaBitQ launch is ordered longest first by predicted cost instead: a pilot search (topk
- * 16, 24 iterations, K 1) gives each query the exact distance of the best row it reaches,
+ * 16, 12 iterations, K 1) gives each query the exact distance of the best row it reaches,
  * and the queries run in descending order of it (the launch of several rounds then ends
  * with short queries).  Results, distances and per-query counters are written at each
  * query's own row as before.  mode 0: off;
