@@ -69,6 +69,7 @@ HIP_API = {
     "bs_debug_beam": (C.c_int, [u32, vp, u32, u32, u32, C.c_int, vp, vp]),
     "bs_debug_sort": (C.c_int, [vp, u32, vp]),
     "bs_debug_cost_order": (C.c_int, [vp, u64, vp, vp]),
+    "bs_debug_label_order": (C.c_int, [vp, vp, u64, u32, u32, vp]),
     "bs_debug_filter": (C.c_int, [C.c_int, u32, vp, u32, u32, vp, vp, u32, vp]),
     "bs_index_groundtruth": (C.c_int, [vp, vp, u64, u32, vp, vp, P(u64)]),
     "bs_index_groundtruth_device": (C.c_int, [vp, vp, u64, u32, vp, vp, vp, P(u64)]),

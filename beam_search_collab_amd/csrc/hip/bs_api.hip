@@ -73,6 +73,8 @@ struct bs_index_s {
     float* d_pnorm = nullptr;
     uint32_t* d_ows = nullptr;  // key[ORDER_CHUNK] | qmap[ORDER_CHUNK] | hist[P] | cursor[P]
     hipEvent_t ws_free = nullptr;
+    // expected cost per label for the base-family label order (calibrate_labels), or null
+    float* d_lcost = nullptr;
     // device staging of bs_search (host buffers): grows to the largest call, reused after
     void* d_stage = nullptr;
     size_t stage_bytes = 0;
@@ -133,6 +135,8 @@ void make_pivots(const float* vecs, uint64_t n, uint32_t dim, std::vector<float>
 }
 // the device address of bs_search_device_noalloc's static workspace (defined below)
 int noalloc_workspace(int dev, uint32_t** out);
+// the label costs of the base-family query order (defined below)
+void calibrate_labels(bs_index ix);
 }  // namespace
 
 extern "C" const char* bs_last_error(void) { return g_err.c_str(); }
@@ -244,6 +248,7 @@ extern "C" int bs_index_create(const float* vecs, const uint32_t* edges, uint64_
         bs_index_destroy(ix);
         return fail(BS_EHIP, std::string("upload failed: ") + hipGetErrorString(e));
     }
+    calibrate_labels(ix);
     *out = ix;
     return BS_OK;
 } catch (...) {
@@ -361,6 +366,7 @@ extern "C" void bs_index_destroy(bs_index ix) {
     if (ix->d_pivT) (void)hipFree(ix->d_pivT);
     if (ix->d_pnorm) (void)hipFree(ix->d_pnorm);
     if (ix->d_ows) (void)hipFree(ix->d_ows);
+    if (ix->d_lcost) (void)hipFree(ix->d_lcost);
     if (ix->d_stage) (void)hipFree(ix->d_stage);
     delete ix;
 }
@@ -565,6 +571,72 @@ hipError_t launch(const Plan& pl, hipStream_t s) {
     }
 }
 
+// Expected cost per pivot label, for the base-family label order (order_one_cost: inside each
+// XCD's run of labels the costliest go first).  CAL_ROWS rows of the index (evenly spaced
+// ids) are searched as queries in base mode (topk CAL_T, K 1, filter 1024, reset 16) from the
+// reference's entry point (compute_entry_point), and their iterations averaged per label: a
+// property of the index's regions, independent of the queries later searched.  Config B
+// (1M x 128, 10k queries, topk 256), launch by the label order 4.26 ms, with the labels of
+// each run by these costs 4.05 ms (by the mean cost of the searched queries themselves 4.01;
+// Spearman +0.91 between the two); the calibration takes ~6 ms once per index.  Any failure
+// leaves d_lcost null, i.e. the plain label order.
+constexpr uint32_t CAL_ROWS = 16384, CAL_T = 64;
+void calibrate_labels(bs_index ix) {
+    uint32_t entry = 0;
+    if (bs_index_entry_point(ix, &entry) != BS_OK) return;
+    const uint32_t m = static_cast<uint32_t>(std::min<uint64_t>({CAL_ROWS, ix->n, (8ull << 20) / ix->dim}));
+    float* q = nullptr;
+    float* lc = nullptr;
+    uint32_t *key = nullptr, *res = nullptr, *pq = nullptr;
+    hipError_t e = hipMalloc(&q, static_cast<size_t>(m) * ix->dim * sizeof(float));
+    if (e == hipSuccess) e = hipMalloc(&key, m * sizeof(uint32_t));
+    if (e == hipSuccess) e = hipMalloc(&res, m * sizeof(uint32_t));
+    if (e == hipSuccess) e = hipMalloc(&pq, static_cast<size_t>(m) * 5 * sizeof(uint32_t));
+    if (e == hipSuccess) e = hipMalloc(&lc, bso::ORDER_P * sizeof(float));
+    if (e == hipSuccess) e = bso::launch_gather_rows(ix->d_vecs, ix->dstride, ix->dim, ix->n, m, q, nullptr);
+    if (e == hipSuccess) {
+        bso::OrderParams o;
+        std::memset(&o, 0, sizeof(o));
+        o.queries = q;
+        o.nq = m;
+        o.dim = ix->dim;
+        o.pivT = ix->d_pivT;
+        o.pnorm = ix->d_pnorm;
+        o.key = key;
+        e = bso::launch_labels(o, nullptr);
+    }
+    if (e == hipSuccess) {
+        bs_search_cfg c;
+        std::memset(&c, 0, sizeof(c));
+        c.mode = BS_BASE;
+        c.K = 1;
+        c.topk_size = CAL_T;
+        c.filter_capacity = 1024;
+        c.entry_point = entry;
+        c.max_iterations = 1024;
+        c.reset_interval = 16;
+        c.queries_per_group = 1;
+        Plan pl;
+        e = make_plan(ix, &c, m, pl) == BS_OK ? hipSuccess : hipErrorInvalidValue;
+        if (e == hipSuccess) {
+            pl.p.queries = q;
+            pl.p.results = res;
+            pl.p.per_query = pq;
+            e = launch(pl, nullptr);
+        }
+    }
+    if (e == hipSuccess) e = bso::launch_label_cost(key, pq, m, lc, nullptr);
+    if (e == hipSuccess) e = hipStreamSynchronize(nullptr);
+    for (void* b : {static_cast<void*>(q), static_cast<void*>(key), static_cast<void*>(res), static_cast<void*>(pq)})
+        if (b) (void)hipFree(b);
+    if (e == hipSuccess) {
+        ix->d_lcost = lc;
+    } else {
+        if (lc) (void)hipFree(lc);
+        (void)hipGetLastError();  // the plain label order stays; the error is not the caller's
+    }
+}
+
 // RaBitQ launches are ordered by predicted cost, longest first, instead of by label.  A
 // query's iteration count varies (config C, topk 600, 10k queries: p50 640, p99 916, max
 // 1024) and a launch of several rounds ends with its last-started long queries; locality
@@ -622,15 +694,8 @@ hipError_t launch_ordered(bs_index ix, Plan pl, uint64_t nq, hipStream_t s, uint
         o.cursor = o.hist + bso::ORDER_P;
         o.g = g;
         o.X = X;
-        // XCD x runs workgroups x, x + X, ...; all are full but the launch's last one
-        const uint64_t B = (m + g - 1) / g;
-        uint64_t acc = 0;
-        for (uint32_t x = 0; x < X; ++x) {
-            o.start[x] = static_cast<uint32_t>(acc);
-            uint64_t cnt = (B > x ? (B - 1 - x) / X + 1 : 0) * g;
-            if ((B - 1) % X == x) cnt -= B * g - m;
-            acc += cnt;
-        }
+        o.lcost = ix->d_lcost;
+        bso::order_starts(o, m);
         if (cost) {
             e = launch_pilot(ix, pl, o.queries, m, ows, s);
             if (e == hipSuccess) e = bso::launch_cost_order(o, s);
@@ -644,7 +709,7 @@ hipError_t launch_ordered(bs_index ix, Plan pl, uint64_t nq, hipStream_t s, uint
         pl.p.per_query = all.per_query ? all.per_query + c0 * 5 : nullptr;
         pl.p.qmap = o.qmap;
         pl.p.nq = m;
-        pl.grid = dim3(static_cast<uint32_t>(B));
+        pl.grid = dim3(static_cast<uint32_t>((m + g - 1) / g));
         e = launch(pl, s);
     }
     if (e == hipSuccess && guard) e = hipEventRecord(ix->ws_free, s);

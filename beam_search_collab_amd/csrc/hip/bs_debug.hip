@@ -361,6 +361,39 @@ extern "C" int bs_debug_cost_order(const float* signal, uint64_t n, uint32_t* qm
     return bs_internal_exception();
 }
 
+extern "C" int bs_debug_label_order(const uint32_t* labels, const float* lcost, uint64_t n, uint32_t g, uint32_t X,
+                                    uint32_t* qmap) try {
+    if (n == 0) return BS_OK;
+    if (n > 65536) return dfail(BS_EINVAL, "n must be <= 65536");
+    if (g == 0 || g > 8 || X == 0 || X > bso::ORDER_MAX_X) return dfail(BS_EINVAL, "g must be in 1..8, X in 1..32");
+    for (uint64_t i = 0; i < n; ++i)
+        if (labels[i] >= bso::ORDER_P) return dfail(BS_EINVAL, "labels must be < 256");
+    DevBuf<uint32_t> key, map;
+    DevBuf<float> lc;
+    DTRY(key.alloc(n));
+    DTRY(map.alloc(n));
+    DTRY(hipMemcpy(key.p, labels, n * 4, hipMemcpyHostToDevice));
+    DTRY(hipMemset(map.p, 0xFF, n * 4));
+    if (lcost) {
+        DTRY(lc.alloc(bso::ORDER_P));
+        DTRY(hipMemcpy(lc.p, lcost, bso::ORDER_P * 4, hipMemcpyHostToDevice));
+    }
+    bso::OrderParams o;
+    std::memset(&o, 0, sizeof(o));
+    o.nq = n;
+    o.key = key.p;
+    o.qmap = map.p;
+    o.lcost = lcost ? lc.p : nullptr;
+    o.g = g;
+    o.X = X;
+    bso::order_starts(o, n);
+    DTRY(bso::launch_place(o, nullptr));
+    DTRY(hipMemcpy(qmap, map.p, n * 4, hipMemcpyDeviceToHost));
+    return BS_OK;
+} catch (...) {
+    return bs_internal_exception();
+}
+
 // ---------------------------------------------------------------------------
 // visit filters
 // ---------------------------------------------------------------------------

@@ -276,12 +276,134 @@ __global__ void __launch_bounds__(1024) order_one(const OrderParams o) {
     }
 }
 
+// order_one with per-label expected costs.  Each XCD still gets its contiguous run of the
+// label order (the same queries, so the same locality in its L2), but inside the run the
+// labels go by descending expected cost (ties in label, i.e. tour, order): a launch of
+// several rounds then ends with each XCD's cheapest regions instead of wherever its run
+// happens to end.  key[q] carries the query's XCD in bits 8+ between the passes.
+__global__ void __launch_bounds__(1024) order_one_cost(const OrderParams o) {
+    __shared__ uint32_t cnt[ORDER_P], cur[ORDER_P], lrank[ORDER_P], byrank[ORDER_P];
+    __shared__ float cost[ORDER_P];
+    __shared__ uint32_t off[ORDER_MAX_X * ORDER_P];
+    const uint32_t t = threadIdx.x, X = o.X;
+    if (t < ORDER_P) {
+        cnt[t] = 0u;
+        const float c = o.lcost[t];
+        cost[t] = c - c == 0.0f ? c : 0.0f;  // finite, so that the ranks below are a permutation
+    }
+    for (uint32_t i = t; i < X * ORDER_P; i += 1024) off[i] = 0u;
+    __syncthreads();
+    for (uint64_t q = t; q < o.nq; q += 1024) atomicAdd(&cnt[o.key[q]], 1u);
+    if (t < ORDER_P) {
+        uint32_t r = 0;
+        const float c = cost[t];
+        for (uint32_t j = 0; j < ORDER_P; ++j) r += (cost[j] > c || (cost[j] == c && j < t)) ? 1u : 0u;
+        lrank[t] = r;
+    }
+    __syncthreads();
+    if (t < ORDER_P) byrank[lrank[t]] = t;
+    if (t == 0) {
+        uint32_t a = 0;
+        for (uint32_t b = 0; b < ORDER_P; ++b) {
+            cur[b] = a;
+            a += cnt[b];
+        }
+    }
+    __syncthreads();
+    // each query's XCD: the run its rank in the label order falls in
+    for (uint64_t q = t; q < o.nq; q += 1024) {
+        const uint32_t l = o.key[q];
+        const uint32_t r = atomicAdd(&cur[l], 1u);
+        uint32_t x = 0;
+        while (x + 1 < X && o.start[x + 1] <= r) ++x;
+        o.key[q] = l | (x << 8);
+        atomicAdd(&off[x * ORDER_P + l], 1u);
+    }
+    __syncthreads();
+    // inside each run, the labels in rank order
+    if (t < X) {
+        uint32_t a = 0;
+        for (uint32_t k = 0; k < ORDER_P; ++k) {
+            const uint32_t l = byrank[k];
+            const uint32_t c = off[t * ORDER_P + l];
+            off[t * ORDER_P + l] = a;
+            a += c;
+        }
+    }
+    __syncthreads();
+    for (uint64_t q = t; q < o.nq; q += 1024) {
+        const uint32_t v = o.key[q], l = v & (ORDER_P - 1), x = v >> 8;
+        const uint32_t j = atomicAdd(&off[x * ORDER_P + l], 1u);
+        const uint64_t pos = (x + static_cast<uint64_t>(X) * (j / o.g)) * o.g + j % o.g;
+        if (pos < o.nq) o.qmap[pos] = static_cast<uint32_t>(q);
+        o.key[q] = l;
+    }
+}
+
+__global__ void __launch_bounds__(1024) label_cost(const uint32_t* labels, const uint32_t* per_query, uint32_t n,
+                                                   float* lcost) {
+    __shared__ uint32_t sum[ORDER_P], cnt[ORDER_P];
+    __shared__ unsigned long long all;
+    const uint32_t t = threadIdx.x;
+    if (t < ORDER_P) sum[t] = cnt[t] = 0u;
+    if (t == 0) all = 0ull;
+    __syncthreads();
+    for (uint32_t i = t; i < n; i += 1024) {
+        const uint32_t l = labels[i] & (ORDER_P - 1), it = per_query[static_cast<uint64_t>(i) * 5];
+        atomicAdd(&sum[l], it);
+        atomicAdd(&cnt[l], 1u);
+        atomicAdd(&all, static_cast<unsigned long long>(it));
+    }
+    __syncthreads();
+    if (t < ORDER_P) {
+        const float mean = n ? static_cast<float>(static_cast<double>(all) / n) : 0.0f;
+        lcost[t] = cnt[t] ? static_cast<float>(static_cast<double>(sum[t]) / cnt[t]) : mean;
+    }
+}
+
+__global__ void __launch_bounds__(256) gather_rows(const float* vecs, uint32_t dstride, uint32_t dim, uint64_t n,
+                                                   uint32_t m, float* out) {
+    const uint64_t e = static_cast<uint64_t>(blockIdx.x) * 256 + threadIdx.x;
+    if (e >= static_cast<uint64_t>(m) * dim) return;
+    const uint64_t i = e / dim, k = e - i * dim;
+    out[e] = vecs[(i * n / m) * dstride + k];
+}
+
+hipError_t launch_place(const OrderParams& o, hipStream_t s) {
+    if (o.nq > ONE_WG) return hipErrorInvalidValue;
+    if (o.lcost) hipLaunchKernelGGL(order_one_cost, dim3(1), dim3(1024), 0, s, o);
+    else hipLaunchKernelGGL(order_one, dim3(1), dim3(1024), 0, s, o);
+    return hipGetLastError();
+}
+
+hipError_t launch_labels(const OrderParams& o, hipStream_t s) {
+    if (o.nq > ONE_WG) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(order_key, dim3(static_cast<uint32_t>((o.nq + 31) / 32)), dim3(256), 0, s, o);
+    return hipGetLastError();
+}
+
+hipError_t launch_label_cost(const uint32_t* labels, const uint32_t* per_query, uint32_t n, float* lcost,
+                             hipStream_t s) {
+    hipLaunchKernelGGL(label_cost, dim3(1), dim3(1024), 0, s, labels, per_query, n, lcost);
+    return hipGetLastError();
+}
+
+hipError_t launch_gather_rows(const float* vecs, uint32_t dstride, uint32_t dim, uint64_t n, uint32_t m, float* out,
+                              hipStream_t s) {
+    const uint64_t total = static_cast<uint64_t>(m) * dim;
+    if (total == 0) return hipSuccess;
+    hipLaunchKernelGGL(gather_rows, dim3(static_cast<uint32_t>((total + 255) / 256)), dim3(256), 0, s, vecs, dstride,
+                       dim, n, m, out);
+    return hipGetLastError();
+}
+
 hipError_t launch_order(const OrderParams& o, hipStream_t s) {
     hipLaunchKernelGGL(order_key, dim3(static_cast<uint32_t>((o.nq + 31) / 32)), dim3(256), 0, s, o);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     if (o.nq <= ONE_WG) {
-        hipLaunchKernelGGL(order_one, dim3(1), dim3(1024), 0, s, o);
+        if (o.lcost) hipLaunchKernelGGL(order_one_cost, dim3(1), dim3(1024), 0, s, o);
+        else hipLaunchKernelGGL(order_one, dim3(1), dim3(1024), 0, s, o);
         return hipGetLastError();
     }
     hipLaunchKernelGGL(order_scan, dim3(1), dim3(ORDER_P), 0, s, o);

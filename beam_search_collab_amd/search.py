@@ -297,6 +297,18 @@ def debug_cost_order(signal):
     return qmap, bucket
 
 
+def debug_label_order(labels, lcost, g, X):
+    """qmap of the base-family query order for given labels and per-label costs (None: plain label
+    order); bs_debug_label_order"""
+    labels = np.ascontiguousarray(labels, dtype=np.uint32)
+    n = labels.shape[0]
+    qmap = np.empty(n, np.uint32)
+    lc = None if lcost is None else np.ascontiguousarray(lcost, dtype=np.float32)
+    _check(_lib.hip().bs_debug_label_order(_ptr(labels), _ptr(lc) if lc is not None else None, n, g, X, _ptr(qmap)),
+           "bs_debug_label_order")
+    return qmap
+
+
 def debug_mfma32(A, B):
     A = np.ascontiguousarray(A, dtype=np.float32).reshape(32, 2)
     B = np.ascontiguousarray(B, dtype=np.float32).reshape(2, 32)

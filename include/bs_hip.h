@@ -243,6 +243,15 @@ int bs_debug_sort(const uint64_t* keys, uint32_t n, uint64_t* out);
  * reference (its launches run query i in block i). */
 int bs_debug_cost_order(const float* signal, uint64_t n, uint32_t* qmap, uint32_t* bucket);
 
+/* The placement of the base-family query order for n (<= 65536) queries with the given pivot
+ * labels (host, < 256), g queries per workgroup (1..8) and X XCDs (1..32): qmap[p] = the query
+ * at launch position p.  Workgroup b runs on XCD b mod X; XCD x gets the x-th contiguous run
+ * of the queries sorted by label.  lcost (host, 256 expected costs per label, or NULL): inside
+ * each run the labels go by descending cost, ties in label order.  No counterpart in the
+ * reference (its launches run query i in block i). */
+int bs_debug_label_order(const uint32_t* labels, const float* lcost, uint64_t n, uint32_t g, uint32_t X,
+                         uint32_t* qmap);
+
 /* One v_mfma_f32_32x32x2f32 product: A 32x2 and B 2x32 row-major in, D = A B 32x32
  * row-major out, read back through the accumulator layout the ground-truth kernel uses. */
 int bs_debug_mfma32(const float* A, const float* B, float* D);

@@ -432,3 +432,35 @@ def test_rabitq_cost_order(gpu):
             assert len(np.unique(b)) > 200, n
     qmap, b = search.debug_cost_order(np.full(1000, 7.0, np.float32))
     assert np.array_equal(np.sort(qmap), np.arange(1000)) and len(np.unique(b)) == 1
+
+
+def test_label_order_placement(gpu):
+    """the base-family query order (bs_debug_label_order): the launch map is a permutation; XCD x
+    (the workgroups b with b mod X == x) gets the x-th contiguous run of the queries sorted by
+    label, with or without per-label costs; along an XCD's positions the labels ascend (plain) or
+    follow descending cost, ties in label order (with costs; a NaN cost counts as 0)"""
+    rng = np.random.default_rng(31)
+    for n, g, X in ((1, 1, 8), (7, 1, 8), (1000, 1, 8), (1000, 2, 8), (4097, 4, 8), (65536, 1, 8), (300, 1, 3),
+                    (5000, 8, 32)):
+        labels = rng.integers(0, 256, n).astype(np.uint32)
+        labels[labels % 7 == 3] = 5  # absent labels and a crowded one
+        cost = rng.gamma(3.0, 100.0, 256).astype(np.float32)
+        cost[[1, 2, 3]] = cost[0]  # ties
+        cost[9] = np.nan
+        ckey = np.where(np.isnan(cost), 0.0, cost)
+        pos = np.arange(n)
+        xcd = (pos // g) % X
+        sizes = np.array([(xcd == x).sum() for x in range(X)])
+        start = np.concatenate([[0], np.cumsum(sizes)])
+        sorted_labels = np.sort(labels)
+        for lc in (None, cost):
+            qm = search.debug_label_order(labels, lc, g, X)
+            assert np.array_equal(np.sort(qm), np.arange(n)), (n, g, X)
+            for x in range(X):
+                seq = labels[qm[xcd == x]]
+                assert np.array_equal(np.sort(seq), sorted_labels[start[x]:start[x + 1]]), (n, g, X, x)
+                if lc is None:
+                    assert (np.diff(seq.astype(np.int64)) >= 0).all(), (n, g, X, x)
+                else:
+                    k = list(zip(-ckey[seq], seq))
+                    assert k == sorted(k), (n, g, X, x)
