@@ -84,7 +84,10 @@ typedef struct {
 
 /* Upload a graph: vecs n*dim f32, edges n*degree u32 (ids < n or 0xFFFFFFFF).
  * Replaces GPUGraph(const CPUGraph&) (gpu_graph.cuh:81-146).  Validates every edge on
- * the host.  dim 1..1024, degree 1..256 (the reference gpu_cli's range), n < 2^31. */
+ * the host.  dim 1..1024, degree 1..256 (the reference gpu_cli's range), n < 2^31.  Also
+ * prepares the query scheduling: 256 pivot rows, and the expected search cost per pivot
+ * region (about 7 ms at 1M x 128: the entry point and a base search of 16384 index rows;
+ * without it, which a failure there leaves, the scheduling uses the plain label order). */
 int bs_index_create(const float* vecs, const uint32_t* edges, uint64_t n, uint32_t dim,
                     uint32_t degree, bs_index* out);
 
@@ -138,7 +141,10 @@ int bs_search_device_noalloc(bs_index idx, const bs_search_cfg* cfg, const float
  * changes no result; it changes where their gathers hit and when the launch ends.  With
  * scheduling on, a base / warp / bwarp launch first labels each query with its nearest of
  * 256 pivot rows (fixed at bs_index_create), sorts the queries by label and gives each XCD
- * a contiguous run of them, so queries that walk the same region share that XCD's L2.  A
+ * a contiguous run of them, so queries that walk the same region share that XCD's L2; inside
+ * a run (launches of up to 65536 queries) the labels go by descending expected cost, which
+ * bs_index_create calibrates once (16384 index rows searched in base mode from the
+ * reference's entry point, iterations averaged per label).  A
  * RaBitQ launch is ordered longest first by predicted cost instead: a pilot search (topk
  * 16, 12 iterations, K 1) gives each query the exact distance of the best row it reaches,
  * and the queries run in descending order of it (the launch of several rounds then ends
