@@ -22,6 +22,23 @@ using namespace bsw;
 // cost_order_one): LDS counts and placement instead of global atomics and more launches
 constexpr uint64_t ONE_WG = 65536;
 
+// The one-workgroup kernels read their queries' keys in batches of KCH loads per thread, all
+// issued before any is used (a few global round trips per pass instead of one per query the
+// thread handles); nothing per query stays in registers between passes (64 queries per
+// thread would not fit), what a later pass needs goes back to the key array.
+constexpr int KPT = static_cast<int>(ONE_WG / 1024);  // queries per thread at most
+constexpr int KCH = 16;                               // loads in flight per thread
+
+// v[j] = key of query t + 1024 (c + j) (fill for queries past nq)
+__device__ __forceinline__ void load_batch(const OrderParams& o, int c, uint32_t fill, uint32_t (&v)[KCH]) {
+    const uint64_t t = threadIdx.x;
+#pragma unroll
+    for (int j = 0; j < KCH; ++j) {
+        const uint64_t q = t + 1024ull * static_cast<uint32_t>(c + j);
+        v[j] = q < o.nq ? o.key[q] : fill;
+    }
+}
+
 __device__ __forceinline__ uint32_t orderable(float f) {
     const uint32_t b = __float_as_uint(f);
     return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
@@ -206,19 +223,71 @@ __global__ void __launch_bounds__(256) cost_key(const OrderParams o) {
 
 // The whole cost order in one workgroup, for launches of up to ONE_WG queries: range,
 // buckets and counts in LDS, the scan, the placement (4 launches and their global atomics
-// took 0.07 ms at 10k queries).  Leaves hist and cursor untouched.
+// took 0.07 ms at 10k queries), with the signals in registers.  key[q] gets the bucket;
+// hist and cursor are left untouched.
+// cost_moments over the launch's signals, read in batches
+__device__ __forceinline__ void batch_moments(const OrderParams& o, double clo, double chi, double* s1, double* s2,
+                                              double* sn, double& mu, double& sd) {
+    const uint32_t t = threadIdx.x;
+    double a = 0.0, b = 0.0, n = 0.0;
+#pragma unroll 1
+    for (int c = 0; c < KPT && t + 1024ull * c < o.nq; c += KCH) {
+        uint32_t v[KCH];
+        load_batch(o, c, 0x7FC00000u, v);  // NaN past nq: not counted
+#pragma unroll
+        for (int j = 0; j < KCH; ++j) {
+            const double d = __uint_as_float(v[j]);
+            if (d >= clo && d <= chi) {  // false for NaN
+                a += d;
+                b += d * d;
+                n += 1.0;
+            }
+        }
+    }
+    s1[t] = a;
+    s2[t] = b;
+    sn[t] = n;
+    __syncthreads();
+    for (uint32_t h = 512; h > 0; h >>= 1) {
+        if (t < h) {
+            s1[t] += s1[t + h];
+            s2[t] += s2[t + h];
+            sn[t] += sn[t + h];
+        }
+        __syncthreads();
+    }
+    mu = sn[0] > 0.0 ? s1[0] / sn[0] : 0.0;
+    const double var = sn[0] > 0.0 ? s2[0] / sn[0] - mu * mu : 0.0;
+    sd = var > 0.0 ? sqrt(var) : 0.0;
+    __syncthreads();
+}
+
 __global__ void __launch_bounds__(1024) cost_order_one(const OrderParams o) {
     __shared__ double s1[1024], s2[1024], sn[1024];
     __shared__ uint32_t cnt[ORDER_P], cur[ORDER_P];
     const uint32_t t = threadIdx.x;
-    float lo, hi;
-    cost_bounds<1024>(o, s1, s2, sn, lo, hi);
+    const double fmax = 3.4028234663852886e38;
+    double mu, sd;
+    batch_moments(o, -fmax, fmax, s1, s2, sn, mu, sd);
+    batch_moments(o, mu - 3.0 * sd, mu + 3.0 * sd, s1, s2, sn, mu, sd);
+    const float lo = static_cast<float>(mu - 2.0 * sd);
+    float hi = static_cast<float>(mu + 2.0 * sd);
+    if (!(hi > lo)) hi = lo + 1.0f;
     if (t < ORDER_P) cnt[t] = 0u;
     __syncthreads();
-    for (uint64_t q = t; q < o.nq; q += 1024) {
-        const uint32_t b = cost_bucket(__uint_as_float(o.key[q]), lo, hi);
-        o.key[q] = b;
-        atomicAdd(&cnt[b], 1u);
+#pragma unroll 1
+    for (int c = 0; c < KPT && t + 1024ull * c < o.nq; c += KCH) {
+        uint32_t v[KCH];
+        load_batch(o, c, 0u, v);
+#pragma unroll
+        for (int j = 0; j < KCH; ++j) {
+            const uint64_t q = t + 1024ull * (c + j);
+            if (q < o.nq) {
+                const uint32_t b = cost_bucket(__uint_as_float(v[j]), lo, hi);
+                o.key[q] = b;
+                atomicAdd(&cnt[b], 1u);
+            }
+        }
     }
     __syncthreads();
     if (t == 0) {
@@ -229,7 +298,16 @@ __global__ void __launch_bounds__(1024) cost_order_one(const OrderParams o) {
         }
     }
     __syncthreads();
-    for (uint64_t q = t; q < o.nq; q += 1024) o.qmap[atomicAdd(&cur[o.key[q]], 1u)] = static_cast<uint32_t>(q);
+#pragma unroll 1
+    for (int c = 0; c < KPT && t + 1024ull * c < o.nq; c += KCH) {
+        uint32_t v[KCH];
+        load_batch(o, c, 0u, v);
+#pragma unroll
+        for (int j = 0; j < KCH; ++j) {
+            const uint64_t q = t + 1024ull * (c + j);
+            if (q < o.nq) o.qmap[atomicAdd(&cur[v[j]], 1u)] = static_cast<uint32_t>(q);
+        }
+    }
 }
 
 hipError_t launch_cost_order(const OrderParams& o, hipStream_t s) {
@@ -260,7 +338,14 @@ __global__ void __launch_bounds__(1024) order_one(const OrderParams o) {
     const uint32_t t = threadIdx.x;
     if (t < ORDER_P) cnt[t] = 0u;
     __syncthreads();
-    for (uint64_t q = t; q < o.nq; q += 1024) atomicAdd(&cnt[o.key[q]], 1u);
+#pragma unroll 1
+    for (int c = 0; c < KPT && t + 1024ull * c < o.nq; c += KCH) {
+        uint32_t v[KCH];
+        load_batch(o, c, 0u, v);
+#pragma unroll
+        for (int j = 0; j < KCH; ++j)
+            if (t + 1024ull * (c + j) < o.nq) atomicAdd(&cnt[v[j]], 1u);
+    }
     __syncthreads();
     if (t == 0) {
         uint32_t a = 0;
@@ -270,9 +355,18 @@ __global__ void __launch_bounds__(1024) order_one(const OrderParams o) {
         }
     }
     __syncthreads();
-    for (uint64_t q = t; q < o.nq; q += 1024) {
-        const uint64_t pos = order_pos(o, atomicAdd(&cur[o.key[q]], 1u));
-        if (pos < o.nq) o.qmap[pos] = static_cast<uint32_t>(q);
+#pragma unroll 1
+    for (int c = 0; c < KPT && t + 1024ull * c < o.nq; c += KCH) {
+        uint32_t v[KCH];
+        load_batch(o, c, 0u, v);
+#pragma unroll
+        for (int j = 0; j < KCH; ++j) {
+            const uint64_t q = t + 1024ull * (c + j);
+            if (q < o.nq) {
+                const uint64_t pos = order_pos(o, atomicAdd(&cur[v[j]], 1u));
+                if (pos < o.nq) o.qmap[pos] = static_cast<uint32_t>(q);
+            }
+        }
     }
 }
 
@@ -280,7 +374,7 @@ __global__ void __launch_bounds__(1024) order_one(const OrderParams o) {
 // label order (the same queries, so the same locality in its L2), but inside the run the
 // labels go by descending expected cost (ties in label, i.e. tour, order): a launch of
 // several rounds then ends with each XCD's cheapest regions instead of wherever its run
-// happens to end.  key[q] carries the query's XCD in bits 8+ between the passes.
+// happens to end.  A query's key in registers carries its XCD in bits 8+ between the passes.
 __global__ void __launch_bounds__(1024) order_one_cost(const OrderParams o) {
     __shared__ uint32_t cnt[ORDER_P], cur[ORDER_P], lrank[ORDER_P], byrank[ORDER_P];
     __shared__ float cost[ORDER_P];
@@ -293,7 +387,14 @@ __global__ void __launch_bounds__(1024) order_one_cost(const OrderParams o) {
     }
     for (uint32_t i = t; i < X * ORDER_P; i += 1024) off[i] = 0u;
     __syncthreads();
-    for (uint64_t q = t; q < o.nq; q += 1024) atomicAdd(&cnt[o.key[q]], 1u);
+#pragma unroll 1
+    for (int c = 0; c < KPT && t + 1024ull * c < o.nq; c += KCH) {
+        uint32_t v[KCH];
+        load_batch(o, c, 0u, v);
+#pragma unroll
+        for (int j = 0; j < KCH; ++j)
+            if (t + 1024ull * (c + j) < o.nq) atomicAdd(&cnt[v[j]], 1u);
+    }
     if (t < ORDER_P) {
         uint32_t r = 0;
         const float c = cost[t];
@@ -310,14 +411,23 @@ __global__ void __launch_bounds__(1024) order_one_cost(const OrderParams o) {
         }
     }
     __syncthreads();
-    // each query's XCD: the run its rank in the label order falls in
-    for (uint64_t q = t; q < o.nq; q += 1024) {
-        const uint32_t l = o.key[q];
-        const uint32_t r = atomicAdd(&cur[l], 1u);
-        uint32_t x = 0;
-        while (x + 1 < X && o.start[x + 1] <= r) ++x;
-        o.key[q] = l | (x << 8);
-        atomicAdd(&off[x * ORDER_P + l], 1u);
+    // each query's XCD: the run its rank in the label order falls in (kept in key bits 8+)
+#pragma unroll 1
+    for (int c = 0; c < KPT && t + 1024ull * c < o.nq; c += KCH) {
+        uint32_t v[KCH];
+        load_batch(o, c, 0u, v);
+#pragma unroll
+        for (int j = 0; j < KCH; ++j) {
+            const uint64_t q = t + 1024ull * (c + j);
+            if (q < o.nq) {
+                const uint32_t l = v[j];
+                const uint32_t r = atomicAdd(&cur[l], 1u);
+                uint32_t x = 0;
+                while (x + 1 < X && o.start[x + 1] <= r) ++x;
+                o.key[q] = l | (x << 8);
+                atomicAdd(&off[x * ORDER_P + l], 1u);
+            }
+        }
     }
     __syncthreads();
     // inside each run, the labels in rank order
@@ -325,18 +435,27 @@ __global__ void __launch_bounds__(1024) order_one_cost(const OrderParams o) {
         uint32_t a = 0;
         for (uint32_t k = 0; k < ORDER_P; ++k) {
             const uint32_t l = byrank[k];
-            const uint32_t c = off[t * ORDER_P + l];
+            const uint32_t n = off[t * ORDER_P + l];
             off[t * ORDER_P + l] = a;
-            a += c;
+            a += n;
         }
     }
     __syncthreads();
-    for (uint64_t q = t; q < o.nq; q += 1024) {
-        const uint32_t v = o.key[q], l = v & (ORDER_P - 1), x = v >> 8;
-        const uint32_t j = atomicAdd(&off[x * ORDER_P + l], 1u);
-        const uint64_t pos = (x + static_cast<uint64_t>(X) * (j / o.g)) * o.g + j % o.g;
-        if (pos < o.nq) o.qmap[pos] = static_cast<uint32_t>(q);
-        o.key[q] = l;
+#pragma unroll 1
+    for (int c = 0; c < KPT && t + 1024ull * c < o.nq; c += KCH) {
+        uint32_t v[KCH];
+        load_batch(o, c, 0u, v);
+#pragma unroll
+        for (int j = 0; j < KCH; ++j) {
+            const uint64_t q = t + 1024ull * (c + j);
+            if (q < o.nq) {
+                const uint32_t l = v[j] & (ORDER_P - 1), x = v[j] >> 8;
+                const uint32_t i = atomicAdd(&off[x * ORDER_P + l], 1u);
+                const uint64_t pos = (x + static_cast<uint64_t>(X) * (i / o.g)) * o.g + i % o.g;
+                if (pos < o.nq) o.qmap[pos] = static_cast<uint32_t>(q);
+                o.key[q] = l;
+            }
+        }
     }
 }
 
