@@ -60,6 +60,7 @@ HIP_API = {
     "bs_index_info": (C.c_int, [vp, P(u64), P(u32), P(u32), P(u32), P(C.c_int)]),
     "bs_index_destroy": (None, [vp]),
     "bs_index_set_query_order": (C.c_int, [vp, C.c_int]),
+    "bs_index_label_costs": (C.c_int, [vp, vp]),
     "bs_index_entry_point": (C.c_int, [vp, P(u32)]),
     "bs_index_build_rabitq": (C.c_int, [vp, u32, vp, vp, vp, P(u32)]),
     "bs_build_vamana_device": (C.c_int, [vp, u64, u32, u32, u32, f32, u32, vp, C.c_int]),

@@ -371,6 +371,15 @@ extern "C" void bs_index_destroy(bs_index ix) {
     delete ix;
 }
 
+extern "C" int bs_index_label_costs(bs_index ix, float* out) try {
+    if (!ix || !out) return fail(BS_EINVAL, "null argument");
+    if (!ix->d_lcost) return fail(BS_EINVAL, "the index has no calibrated label costs");
+    HIP_TRY(hipMemcpy(out, ix->d_lcost, bso::ORDER_P * sizeof(float), hipMemcpyDeviceToHost));
+    return BS_OK;
+} catch (...) {
+    return bs_internal_exception();
+}
+
 extern "C" int bs_index_set_query_order(bs_index ix, int mode) try {
     if (!ix) return fail(BS_EINVAL, "null index");
     if (mode < 0 || mode > 2) return fail(BS_EINVAL, "query order mode must be 0, 1 or 2");

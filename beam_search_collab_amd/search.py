@@ -114,6 +114,13 @@ class GPUGraph:
         """0 off, 1 on for batches of >= 4096 queries (default), 2 always (bs_index_set_query_order)."""
         _check(_lib.hip().bs_index_set_query_order(self._h, mode), "bs_index_set_query_order")
 
+    def label_costs(self) -> np.ndarray:
+        """the expected search cost per pivot label calibrated at index creation
+        (bs_index_label_costs), 256 floats"""
+        out = np.empty(256, np.float32)
+        _check(_lib.hip().bs_index_label_costs(self._h, _ptr(out)), "bs_index_label_costs")
+        return out
+
     @property
     def handle(self):
         return self._h

@@ -155,6 +155,12 @@ int bs_search_device_noalloc(bs_index idx, const bs_search_cfg* cfg, const float
  * on another stream waits for the previous scheduled call on the device. */
 int bs_index_set_query_order(bs_index idx, int mode);
 
+/* The expected search cost per pivot label that bs_index_create calibrated (mean iterations of
+ * the calibration search's queries of each label; labels without one get the mean of all):
+ * out[256] (host).  BS_EINVAL when the index has none (the calibration failed), in which case
+ * the base-family order is the plain label order.  No counterpart in the reference. */
+int bs_index_label_costs(bs_index idx, float* out);
+
 /* The search entry point of the uploaded index, computed on the device: compute_entry_point
  * (src/gpu_cli.cu:55-83) -- the float centroid accumulated row by row, then the first row of
  * least float squared distance to it -- with the same float roundings, so *entry equals

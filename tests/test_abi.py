@@ -60,6 +60,7 @@ def test_argument_errors_before_any_device_call():
     cfg = _lib.SearchCfg(0, 1, 10, 64, 1024, 0, 1024, 16)
     assert lib.bs_search_device(None, C.byref(cfg), None, 1, None, None, None, None, 0, None) == -1
     assert lib.bs_index_set_query_order(None, 1) == -1
+    assert lib.bs_index_label_costs(None, None) == -1
     e = C.c_uint32()
     assert lib.bs_index_entry_point(None, C.byref(e)) == -1
     out = (C.c_uint32 * 4)()

@@ -464,3 +464,27 @@ def test_label_order_placement(gpu):
                 else:
                     k = list(zip(-ckey[seq], seq))
                     assert k == sorted(k), (n, g, X, x)
+
+
+def test_label_costs_calibration(gpu):
+    """bs_index_create's per-label cost calibration (bs_index_label_costs): every label gets a
+    finite mean iteration count within the calibration search's limits (labels without a
+    calibration row get the mean of all), the costs vary across the regions of a clustered
+    index, and their mean lies within the iteration counts of the same calibration search
+    (the index's rows i*n/m as queries, base mode, topk 64, K 1, from the entry point)"""
+    ds = dataset(3000, 64, 32, 10)
+    g, base = ds["g"], ds["base"]
+    c = g.label_costs()
+    assert c.shape == (256,) and np.isfinite(c).all()
+    assert (c >= 1).all() and (c <= 1024).all()
+    assert c.std() > 0
+    n = base.shape[0]
+    m = min(16384, n)
+    rows = base[(np.arange(m, dtype=np.int64) * n) // m]
+    entry = g.entry_point()
+    _, _, st = g.search(rows, 1, "base", GPUBaseSearchCfg(64, 1024, entry, 1024, 16))
+    mean_it = st["iterations"] / m
+    assert c.min() <= mean_it + 1e-3 and mean_it - 1e-3 <= c.max()
+    tiny = dataset(40, 32, 8, 5)  # fewer rows than pivots: every label still has a cost
+    ct = tiny["g"].label_costs()
+    assert np.isfinite(ct).all() and (ct >= 1).all()
