@@ -406,7 +406,7 @@ int make_plan(bs_index ix, const bs_search_cfg* cfg, uint64_t nq, Plan& pl) {
     if (mode < BS_BASE || mode > BS_RABITQ) return fail(BS_EINVAL, "unknown mode " + std::to_string(mode));
     if (mode == BS_RABITQ && !ix->d_recs) return fail(BS_EINVAL, "rabitq mode needs bs_index_attach_rabitq first");
     const uint32_t T = cfg->topk_size;
-    if (T == 0 || T > 1024) return fail(BS_EINVAL, "topk_size must be in 1..1024");
+    if (T == 0 || T > 4096) return fail(BS_EINVAL, "topk_size must be in 1..4096");
     if (cfg->K == 0) return fail(BS_EINVAL, "K must be >= 1");
     if (mode != BS_RABITQ && T < cfg->K)
         return fail(BS_EINVAL, "topk_size (" + std::to_string(T) + ") must be >= K (" + std::to_string(cfg->K) + ")");
@@ -424,7 +424,8 @@ int make_plan(bs_index ix, const bs_search_cfg* cfg, uint64_t nq, Plan& pl) {
     // RaBitQ beams of 513..640 and 641..768 keys get 10 and 12 registers (the recall@10 0.95
     // point of config C is topk 640: 1M x 128, 10k queries, 6.31 ms with 12 registers)
     pl.TR = T <= 64 ? 1 : T <= 128 ? 2 : T <= 256 ? 4 : T <= 512 ? 8
-          : (T <= 640 && mode == BS_RABITQ) ? 10 : (T <= 768 && mode == BS_RABITQ) ? 12 : 16;
+          : (T <= 640 && mode == BS_RABITQ) ? 10 : (T <= 768 && mode == BS_RABITQ) ? 12
+          : T <= 1024 ? 16 : T <= 2048 ? 32 : 64;
     pl.CR = ix->degree <= 64 ? 1 : ix->degree <= 128 ? 2 : 4;
     bsd::L2Shape L = bsd::l2_shape(ix->dim);
     if (L.QR > 4) return fail(BS_EINVAL, "dim too large");

@@ -261,7 +261,7 @@ static void launch_beam_c(int CR, int run, uint32_t T, const uint64_t* k, uint32
 
 extern "C" int bs_debug_beam(uint32_t topk, const uint64_t* keys, uint32_t nbatch, uint32_t bsize, uint32_t picks,
                              int pick_run, uint32_t* picked, uint64_t* beam_out) try {
-    if (topk == 0 || topk > 1024) return dfail(BS_EINVAL, "topk must be in 1..1024");
+    if (topk == 0 || topk > 4096) return dfail(BS_EINVAL, "topk must be in 1..4096");
     if (bsize == 0 || bsize > 128) return dfail(BS_EINVAL, "bsize must be in 1..128");
     DevBuf<uint64_t> dk, db;
     DevBuf<uint32_t> dp;
@@ -272,7 +272,7 @@ extern "C" int bs_debug_beam(uint32_t topk, const uint64_t* keys, uint32_t nbatc
     if (nk) DTRY(hipMemcpy(dk.p, keys, nk * 8, hipMemcpyHostToDevice));
     // the search kernel's beam sizes, with the RaBitQ ones (10 and 12 registers) above 512
     const int TR = topk <= 64 ? 1 : topk <= 128 ? 2 : topk <= 256 ? 4 : topk <= 512 ? 8 : topk <= 640 ? 10
-                 : topk <= 768 ? 12 : 16;
+                 : topk <= 768 ? 12 : topk <= 1024 ? 16 : topk <= 2048 ? 32 : 64;
     const int CR = bsize <= 64 ? 1 : 2;
     switch (TR) {
     case 1: launch_beam_c<1>(CR, pick_run, topk, dk.p, nbatch, bsize, picks, dp.p, db.p); break;
@@ -281,7 +281,9 @@ extern "C" int bs_debug_beam(uint32_t topk, const uint64_t* keys, uint32_t nbatc
     case 8: launch_beam_c<8>(CR, pick_run, topk, dk.p, nbatch, bsize, picks, dp.p, db.p); break;
     case 10: launch_beam_c<10>(CR, pick_run, topk, dk.p, nbatch, bsize, picks, dp.p, db.p); break;
     case 12: launch_beam_c<12>(CR, pick_run, topk, dk.p, nbatch, bsize, picks, dp.p, db.p); break;
-    default: launch_beam_c<16>(CR, pick_run, topk, dk.p, nbatch, bsize, picks, dp.p, db.p); break;
+    case 16: launch_beam_c<16>(CR, pick_run, topk, dk.p, nbatch, bsize, picks, dp.p, db.p); break;
+    case 32: launch_beam_c<32>(CR, pick_run, topk, dk.p, nbatch, bsize, picks, dp.p, db.p); break;
+    default: launch_beam_c<64>(CR, pick_run, topk, dk.p, nbatch, bsize, picks, dp.p, db.p); break;
     }
     DTRY(hipGetLastError());
     DTRY(hipMemcpy(beam_out, db.p, topk * 8, hipMemcpyDeviceToHost));
@@ -296,6 +298,7 @@ extern "C" int bs_debug_beam(uint32_t topk, const uint64_t* keys, uint32_t nbatc
 // ---------------------------------------------------------------------------
 template <int TR>
 __global__ void __launch_bounds__(64) dbg_sort_kernel(const uint64_t* keys, uint32_t n, uint64_t* out) {
+    extern __shared__ __attribute__((aligned(16))) char smem[];
     const uint32_t lane = bsd::lane_id();
     uint64_t v[TR];
 #pragma unroll
@@ -303,7 +306,7 @@ __global__ void __launch_bounds__(64) dbg_sort_kernel(const uint64_t* keys, uint
         const uint32_t e = static_cast<uint32_t>(r) * 64u + lane;
         v[r] = e < n ? keys[e] : bsd::EMPTY_KEY;
     }
-    bsd::bitonic_sort<TR>(v);
+    bsd::sort_beam<TR>(v, reinterpret_cast<uint64_t*>(smem));  // the rerank's sort
 #pragma unroll
     for (int r = 0; r < TR; ++r) {
         const uint32_t e = static_cast<uint32_t>(r) * 64u + lane;
@@ -313,7 +316,7 @@ __global__ void __launch_bounds__(64) dbg_sort_kernel(const uint64_t* keys, uint
 
 extern "C" int bs_debug_sort(const uint64_t* keys, uint32_t n, uint64_t* out) try {
     if (n == 0) return BS_OK;
-    if (n > 1024) return dfail(BS_EINVAL, "n must be <= 1024");
+    if (n > 4096) return dfail(BS_EINVAL, "n must be <= 4096");
     DevBuf<uint64_t> dk, dout;
     DTRY(dk.alloc(n));
     DTRY(dout.alloc(n));
@@ -322,7 +325,9 @@ extern "C" int bs_debug_sort(const uint64_t* keys, uint32_t n, uint64_t* out) tr
     else if (n <= 128) hipLaunchKernelGGL(dbg_sort_kernel<2>, dim3(1), dim3(64), 0, nullptr, dk.p, n, dout.p);
     else if (n <= 256) hipLaunchKernelGGL(dbg_sort_kernel<4>, dim3(1), dim3(64), 0, nullptr, dk.p, n, dout.p);
     else if (n <= 512) hipLaunchKernelGGL(dbg_sort_kernel<8>, dim3(1), dim3(64), 0, nullptr, dk.p, n, dout.p);
-    else hipLaunchKernelGGL(dbg_sort_kernel<16>, dim3(1), dim3(64), 0, nullptr, dk.p, n, dout.p);
+    else if (n <= 1024) hipLaunchKernelGGL(dbg_sort_kernel<16>, dim3(1), dim3(64), 0, nullptr, dk.p, n, dout.p);
+    else if (n <= 2048) hipLaunchKernelGGL(dbg_sort_kernel<32>, dim3(1), dim3(64), 32 * 512, nullptr, dk.p, n, dout.p);
+    else hipLaunchKernelGGL(dbg_sort_kernel<64>, dim3(1), dim3(64), 64 * 512, nullptr, dk.p, n, dout.p);
     DTRY(hipGetLastError());
     DTRY(hipMemcpy(out, dout.p, n * 8, hipMemcpyDeviceToHost));
     return BS_OK;

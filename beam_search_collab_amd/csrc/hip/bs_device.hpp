@@ -82,10 +82,38 @@ __device__ __forceinline__ BeamState beam_state(const uint64_t (&)[TR]) {
     return st;
 }
 
+// Beams of more than 16 registers (topk 1025..4096): 32 and 64 registers of 64-bit keys.
+// A register index that is not a compile-time constant is a register-indexed move, and the
+// largest register tuple it can address is 32 dwords (16 keys); an array indexed that way
+// beyond that size goes to scratch memory whole.  So every access to a register chosen at
+// run time goes through beam_reg / beam_mark, which for the large beams combine all
+// registers under a uniform mask (about 4 TR instructions) and keep the beam in VGPRs.  The
+// masks are ANDs rather than selects: the compiler folds a chain of selects among array
+// elements into a load from a selected address, which is the run-time index again.
+
 // register r of the beam (wave-uniform r: a register-indexed move, s_set_gpr_idx)
 template <int TR>
 __device__ __forceinline__ uint64_t beam_reg(const uint64_t (&beam)[TR], uint32_t r) {
-    return beam[r];
+    if constexpr (TR <= 16) {
+        return beam[r];
+    } else {
+        uint64_t v = 0;
+#pragma unroll
+        for (int i = 0; i < TR; ++i) v |= beam[i] & (0ull - static_cast<uint64_t>(r == static_cast<uint32_t>(i)));
+        return v;
+    }
+}
+
+// set the mark (key LSB) of the lanes of lm in register r (wave-uniform r)
+template <int TR>
+__device__ __forceinline__ void beam_mark(uint64_t (&beam)[TR], uint32_t r, uint64_t lm) {
+    if constexpr (TR <= 16) {
+        beam[r] |= bsw::lane_in(lm) ? 1ull : 0ull;
+    } else {
+        const uint64_t bit = bsw::lane_in(lm) ? 1ull : 0ull;
+#pragma unroll
+        for (int i = 0; i < TR; ++i) beam[i] |= bit & static_cast<uint64_t>(r == static_cast<uint32_t>(i));
+    }
 }
 
 // The rank loop costs ~2 TR + 6 instructions per candidate, the sorted merge ~250 plus LDS
@@ -190,7 +218,7 @@ __device__ __forceinline__ void beam_merge(uint64_t (&beam)[TR], const uint64_t 
                                            const uint64_t (&cmask_in)[CR], uint32_t T,
                                            uint64_t* lds_scratch, uint64_t* lds_aux, BeamState& st) {
     const uint32_t lane = lane_id();
-    const uint64_t thr = readlane64(beam[(T - 1) >> 6], (T - 1) & 63u);
+    const uint64_t thr = readlane64(beam_reg<TR>(beam, (T - 1) >> 6), (T - 1) & 63u);
     uint64_t cmask[CR];
     uint32_t n = 0;
 #pragma unroll
@@ -351,7 +379,7 @@ __device__ __forceinline__ uint32_t beam_pick(uint64_t (&beam)[TR], BeamState& s
         }
     }
     // set the mark (key LSB) of element (qr, ql)
-    beam[qr] |= bsw::lane_in(1ull << ql) ? 1ull : 0ull;
+    beam_mark<TR>(beam, qr, 1ull << ql);
     return key_id(kp);
 }
 
@@ -525,7 +553,7 @@ __device__ __forceinline__ uint32_t pending_pick(uint64_t (&beam)[TR], BeamState
         }
     }
     const uint64_t lm = ml < 64u ? (1ull << ml) : 0ull;
-    beam[mr] |= bsw::lane_in(lm) ? 1ull : 0ull;
+    beam_mark<TR>(beam, mr, lm);
     return key_id(u);
 }
 
@@ -593,14 +621,49 @@ __device__ __forceinline__ void bitonic_sort(uint64_t (&v)[TR]) {
     }
 }
 
-// the same for any register count: counts that are not a power of two sort in the next
-// power of two, padded with EMPTY keys (which sort last)
+// The same network for beams of more than 16 registers (2048 and 4096 keys), run in LDS:
+// unrolled over registers it is more code than the compiler will unroll, and a loop over
+// registers indexes them at run time.  The keys go to S[0, 64 TR) register-major, every step
+// of the network makes its 32 TR compare-exchanges 64 at a time, and the keys come back.
 template <int TR>
-__device__ __forceinline__ void sort_beam(uint64_t (&v)[TR]) {
-    if constexpr ((TR & (TR - 1)) == 0) {
+__device__ __forceinline__ void sort_beam_lds(uint64_t (&v)[TR], uint64_t* S) {
+    const uint32_t lane = lane_id();
+    constexpr uint32_t N = 64u * TR;
+#pragma unroll
+    for (int r = 0; r < TR; ++r) S[static_cast<uint32_t>(r) * 64u + lane] = v[r];
+    wave_sync();
+#pragma unroll 1
+    for (uint32_t k = 2; k <= N; k <<= 1) {
+#pragma unroll 1
+        for (uint32_t j = k >> 1; j >= 1; j >>= 1) {
+            // pair i: elements a (bit j clear) and a + j; ascending where bit k of a is clear
+#pragma unroll 4
+            for (uint32_t i = lane; i < N / 2; i += 64) {
+                const uint32_t a = ((i & ~(j - 1u)) << 1) | (i & (j - 1u));
+                const uint64_t x = S[a], y = S[a + j];
+                const bool sw = (a & k) == 0 ? (y < x) : (x < y);
+                S[a] = sw ? y : x;
+                S[a + j] = sw ? x : y;
+            }
+            wave_sync();
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < TR; ++r) v[r] = S[static_cast<uint32_t>(r) * 64u + lane];
+    wave_sync();
+}
+
+// the same for any register count: counts that are not a power of two sort in the next
+// power of two, padded with EMPTY keys (which sort last); beams of more than 16 registers
+// sort in S (64 TR keys of LDS; unused otherwise)
+template <int TR>
+__device__ __forceinline__ void sort_beam(uint64_t (&v)[TR], uint64_t* S) {
+    if constexpr (TR > 16) {
+        sort_beam_lds<TR>(v, S);
+    } else if constexpr ((TR & (TR - 1)) == 0) {
         bitonic_sort<TR>(v);
     } else {
-        constexpr int P = TR <= 16 ? 16 : 32;
+        constexpr int P = 16;
         uint64_t w[P];
 #pragma unroll
         for (int r = 0; r < P; ++r) w[r] = r < TR ? v[r] : EMPTY_KEY;

@@ -62,7 +62,9 @@ static hipError_t launch_any(const SearchParams& p, int TR, int CR, int PB, dim3
     case 10: return launch_c<10>(p, CR, PB, g, b, lds, s, occ);  // rabitq beams of 513..640
     case 12: return launch_c<12>(p, CR, PB, g, b, lds, s, occ);  // rabitq beams of 641..768
 #endif
-    default: return launch_c<16>(p, CR, PB, g, b, lds, s, occ);
+    case 16: return launch_c<16>(p, CR, PB, g, b, lds, s, occ);
+    case 32: return launch_c<32>(p, CR, PB, g, b, lds, s, occ);  // beams of 1025..2048
+    default: return launch_c<64>(p, CR, PB, g, b, lds, s, occ);  // beams of 2049..4096
     }
 }
 

@@ -485,7 +485,7 @@ search_kernel(const SearchParams p) {
             beam[r] = (e < nvb) ? make_key(rd[e], ids[e]) : EMPTY_KEY;
         }
         wave_sync();
-        sort_beam<TR>(beam);
+        sort_beam<TR>(beam, scratch);
 
         // dedup flush from the smallest (gpu_search_rabitq.cuh:319-339): identical ids
         // carry identical exact distances and are adjacent; the flush's hash set accepts

@@ -57,7 +57,7 @@ typedef struct {
     int32_t mode;               /* bs_mode                                             */
     uint32_t queries_per_group; /* wavefronts (queries) per workgroup: 1,2,4,8; 0 -> 1  */
     uint32_t K;                 /* results per query (>= 1, <= topk_size)              */
-    uint32_t topk_size;         /* beam slots, 1..1024 (see the limits below)          */
+    uint32_t topk_size;         /* beam slots, 1..4096 (see the limits below)          */
     uint32_t filter_capacity;   /* hash slots / Bloom bits (rounded up to a power of 2)*/
     uint32_t entry_point;       /* start node (< n)                                    */
     int32_t max_iterations;     /* >= 0                                                */
@@ -65,10 +65,13 @@ typedef struct {
 } bs_search_cfg;
 
 /* Limits against the reference: degree 1..256 and dim 1..1024 as gpu_cli (gpu_cli.cu:208-233,
- * 340-347).  topk_size 1..1024: the beam is held in at most 16 registers of 64 keys per
- * wavefront (and the RaBitQ expanded set in the wavefront's LDS slice); the reference's
- * SharedBitonicTopK takes any multiple of 32 in shared memory (topk_shared.cuh:272-331).
- * Larger beams are refused with BS_EINVAL rather than run slowly from LDS. */
+ * 340-347).  topk_size 1..4096 (any value, not only multiples of 32): the beam is held in the
+ * wavefront's registers, 64 keys per register, in 1..16 registers up to 1024 keys and in 32 or
+ * 64 above (the RaBitQ expanded set in the wavefront's LDS slice); the reference's
+ * SharedBitonicTopK (topk_shared.cuh:272-331) takes multiples of 32 in shared memory, bounded by
+ * the shared memory per block.  Beams above 4096 are refused with BS_EINVAL.  With topk_size >=
+ * filter_capacity a base search admits no new nodes once its table is full, as the reference's
+ * forgettable filter does: such beams want a larger filter_capacity (at most 65536). */
 
 /* Work counters summed over the queries of one call (the byte model of the roofline:
  * base  B_q = 4d + E*4R + D*4d + 4K;

@@ -75,7 +75,8 @@ def _keys(d, ids):
 
 @pytest.mark.parametrize("topk,bsize", [(16, 16), (64, 32), (100, 32), (128, 64), (256, 64), (256, 128),
                                         (512, 64), (512, 128), (600, 64), (640, 128), (700, 64), (768, 128),
-                                        (1024, 64), (1000, 128)])
+                                        (1024, 64), (1000, 128), (1025, 64), (1536, 128), (2048, 64),
+                                        (2049, 128), (3000, 64), (4096, 128)])
 def test_beam_merge_keeps_smallest(gpu, topk, bsize):
     rng = np.random.default_rng(topk * 7 + bsize)
     n = 4 * max(topk, bsize)
@@ -89,7 +90,8 @@ def test_beam_merge_keeps_smallest(gpu, topk, bsize):
 
 
 @pytest.mark.parametrize("topk,bsize,picks", [(64, 32, 1), (128, 32, 2), (256, 64, 1), (512, 64, 3),
-                                              (100, 16, 2), (600, 64, 2), (768, 32, 3), (1024, 64, 2)])
+                                              (100, 16, 2), (600, 64, 2), (768, 32, 3), (1024, 64, 2),
+                                              (1100, 64, 2), (2048, 128, 3), (2500, 32, 1), (4096, 64, 2)])
 def test_beam_interleaved_pick_no_dup_and_order(gpu, topk, bsize, picks):
     rng = np.random.default_rng(topk + picks)
     n = 8 * topk
@@ -107,24 +109,26 @@ def test_beam_interleaved_pick_no_dup_and_order(gpu, topk, bsize, picks):
     assert len(set(p.tolist())) == len(p) > 0
 
 
-def test_beam_ties_and_run_rule(gpu):
+@pytest.mark.parametrize("topk", [128, 2048, 4096])
+def test_beam_ties_and_run_rule(gpu, topk):
     rng = np.random.default_rng(11)
     # many equal distances, distinct ids: ties are ordered by id
-    d = rng.integers(0, 6, 512).astype(np.float32)
-    keys = _keys(d, rng.permutation(512)).reshape(-1, 64)
-    picked, beam = search.debug_beam(128, keys, 2, 0)
-    opicked, obeam = po.beam_run(128, keys, 2, 0)
+    n = 4 * topk
+    d = rng.integers(0, 6, n).astype(np.float32)
+    keys = _keys(d, rng.permutation(n)).reshape(-1, 64)
+    picked, beam = search.debug_beam(topk, keys, 2, 0)
+    opicked, obeam = po.beam_run(topk, keys, 2, 0)
     assert np.array_equal(picked, opicked)
     assert np.array_equal(beam, obeam)
     # duplicated (dist, id) pairs (the rabitq beam): the run rule
-    keys = _keys(d, rng.integers(0, 40, 512)).reshape(-1, 64)
-    picked, beam = search.debug_beam(128, keys, 2, 1)
-    opicked, obeam = po.beam_run(128, keys, 2, 1)
+    keys = _keys(d, rng.integers(0, topk // 3, n)).reshape(-1, 64)
+    picked, beam = search.debug_beam(topk, keys, 2, 1)
+    opicked, obeam = po.beam_run(topk, keys, 2, 1)
     assert np.array_equal(picked, opicked)
     assert np.array_equal(beam, obeam)
 
 
-@pytest.mark.parametrize("n", [1, 5, 64, 100, 128, 200, 256, 300, 512, 700, 1024])
+@pytest.mark.parametrize("n", [1, 5, 64, 100, 128, 200, 256, 300, 512, 700, 1024, 1025, 2048, 3000, 4096])
 def test_bitonic_sort(gpu, n):
     rng = np.random.default_rng(n)
     keys = rng.integers(0, 2**63, n, dtype=np.uint64)

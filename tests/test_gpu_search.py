@@ -62,6 +62,35 @@ def test_modes_topk_d128(gpu, mode, topk):
     assert_same(*run_both(ds, mode, K, topk), f"{mode} topk={topk}")
 
 
+# Beams above 1024 keys: 32 registers (1025..2048 keys) and 64 (2049..4096), whose run-time
+# register accesses select among all registers, and whose rerank sort runs in LDS.  The visit
+# filter gets more slots than the beam holds, so that the beam, not the filter, sets the work.
+@pytest.mark.parametrize("mode", ["base", "warp2", "bwarp1", "rabitq"])
+@pytest.mark.parametrize("topk", [1025, 1536, 2048, 2049, 3000, 4096])
+def test_large_beams(gpu, mode, topk):
+    ds = dataset(12000, 64, 32, 24)
+    assert_same(*run_both(ds, mode, 100, topk, cap=8192), f"{mode} topk={topk}")
+
+
+# two and four candidate registers (degree 100 and 200) with the large beams, narrow and wide
+# RaBitQ codes (dim 48 and 160)
+@pytest.mark.parametrize("degree,dim", [(100, 160), (200, 48)])
+@pytest.mark.parametrize("mode", ["warp1", "bwarp1", "rabitq"])
+@pytest.mark.parametrize("topk", [2048, 4096])
+def test_large_beams_wide_rows(gpu, degree, dim, mode, topk):
+    ds = dataset(8000, dim, degree, 12)
+    assert_same(*run_both(ds, mode, 100, topk, cap=4096), f"{mode} R={degree} dim={dim} topk={topk}")
+
+
+# every beam slot flushed (K = topk), and beams cut short by the iteration limit
+@pytest.mark.parametrize("mode", ["base", "rabitq"])
+@pytest.mark.parametrize("topk", [2048, 4096])
+@pytest.mark.parametrize("max_it", [0, 5, 300])
+def test_large_beams_full_flush_and_limits(gpu, mode, topk, max_it):
+    ds = dataset(12000, 64, 32, 24)
+    assert_same(*run_both(ds, mode, topk, topk, cap=8192, max_it=max_it), f"{mode} topk={topk} max_it={max_it}")
+
+
 @pytest.mark.parametrize("dim,degree,kind", [(32, 16, "mixture"), (100, 64, "normalized"), (64, 100, "normalized"),
                                              (960, 32, "mixture"), (25, 24, "normalized"), (200, 48, "mixture"),
                                              (300, 32, "mixture")])
@@ -205,7 +234,9 @@ def test_config_errors(gpu):
     with pytest.raises(ValueError):
         g.search(ds["q"], 10, "base", GPUBaseSearchCfg(64, 1024, 10**6, 1024, 16))  # entry out of range
     with pytest.raises(ValueError):
-        g.search(ds["q"], 10, "base", GPUBaseSearchCfg(1025, 1024, 0, 1024, 16))  # topk > 1024
+        g.search(ds["q"], 10, "base", GPUBaseSearchCfg(4097, 1024, 0, 1024, 16))  # topk > 4096
+    with pytest.raises(ValueError):
+        g.search(ds["q"], 10, "rabitq", GPURabitqSearchCfg(4097, 1024, ds["erq"], 1024))
     g2 = search.GPUGraph(ds["base"], ds["edges"])
     with pytest.raises(ValueError):
         g2.search(ds["q"], 10, "rabitq")  # no codebook attached

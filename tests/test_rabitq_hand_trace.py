@@ -91,8 +91,8 @@ CASES = {
                     (19, 8, 9, 17, 18)),
 }
 # the T >= 18 trace holds for every beam size of the kernel: one register (18, 64), two, four,
-# eight, twelve and sixteen (512 and above: the deferred merge)
-LARGE_T = [18, 64, 100, 256, 512, 600, 1024]
+# eight, twelve, sixteen, thirty-two and sixty-four (512 and above: the deferred merge)
+LARGE_T = [18, 64, 100, 256, 512, 600, 1024, 2048, 4096]
 
 
 def build_fixture():
