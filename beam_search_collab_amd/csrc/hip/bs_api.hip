@@ -458,7 +458,12 @@ int make_plan(bs_index ix, const bs_search_cfg* cfg, uint64_t nq, Plan& pl) {
     // 5.0 -> 4.8 ms, topk 512: 20.1 -> 10.9 ms), and up to four times as many as the LDS
     // left by the instance's register-limited residency holds (config B with 32-row L2
     // batches: 2048 slots 4.54 ms, 2624 slots 4.43 ms; smaller tables that admit more
-    // wavefronts lost: 1344 slots at 20 wavefronts per CU 5.0 ms).  The RaBitQ expanded set
+    // wavefronts lost: 1344 slots at 20 wavefronts per CU 5.0 ms).  The slice budget rounds
+    // to 512 B, while gfx950 allocates LDS in 1280-B granules (slices of 12640 B fit 12 per
+    // CU, of 12896 B 11), so config B's 2624-slot table (13152 B) holds 11 wavefronts per CU
+    // of the 12 its registers allow; a table small enough for 12 measured slower (2496 slots,
+    // 12 per CU: 4.19-4.27 ms against 4.09-4.14 for 2560-2816 slots at 11, 4.13-4.16 for
+    // 3072 at 10, 4.5 for 3328 at 9; identical results throughout).  The RaBitQ expanded set
     // ends with about one key per beam slot and gets 5T/3 slots within [cap, 2 cap] (topk
     // 768: 2048 slots 14.0 ms, 1280 slots 12.8 ms: fewer slots, more wavefronts per CU).
     uint32_t scratch = 512u * pl.TR + 16u;  // the beam and the merge's dump slot

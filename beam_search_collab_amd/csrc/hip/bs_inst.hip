@@ -69,6 +69,15 @@ static hipError_t launch_any(const SearchParams& p, int TR, int CR, int PB, dim3
 }
 
 #if BS_INST_MODE == 0
+#ifdef BS_PHASE_CLOCKS
+// the instrumented library's per-query clocks of the hash-filter (base, warp) instances
+// (QueryClock): out[3 q + 0..2] = start, end, hardware id of queries q < n (n <= 65536)
+extern "C" int bs_query_clock_read(unsigned long long* out, uint64_t n) {
+    if (n > QUERY_CLOCK_MAX) return 2;
+    return hipMemcpyFromSymbol(out, HIP_SYMBOL(bs_query_clock), sizeof(unsigned long long) * 3 * n) == hipSuccess ? 0
+                                                                                                             : 1;
+}
+#endif
 hipError_t launch_search_hash(const SearchParams& p, int TR, int CR, int PB, dim3 g, dim3 b, size_t lds,
                               hipStream_t s, int* occ) {
     return launch_any(p, TR, CR, PB, g, b, lds, s, occ);

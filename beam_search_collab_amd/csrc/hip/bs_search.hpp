@@ -73,6 +73,34 @@ struct PhaseClock {
 #endif
 };
 
+// Per-query clocks of the same instrumented build (bs_query_clock_read): for query q < 65536
+// of the last launch, its start and end (s_memrealtime: 100 MHz, one counter for the whole
+// device) and the wavefront's hardware id (HW_ID, XCC_ID in the upper word), written by the
+// query's first wavefront.  The launch's timeline: concurrency, the drain after the last
+// query starts, the XCD and CU each query ran on.
+#ifdef BS_PHASE_CLOCKS
+constexpr uint32_t QUERY_CLOCK_MAX = 65536;
+static __device__ unsigned long long bs_query_clock[QUERY_CLOCK_MAX * 3];
+#endif
+struct QueryClock {
+#ifdef BS_PHASE_CLOCKS
+    uint64_t t0 = 0;
+    __device__ __forceinline__ void start() { t0 = __builtin_amdgcn_s_memrealtime(); }
+    __device__ __forceinline__ void finish(uint64_t qid, bool writer) {
+        const uint64_t t1 = __builtin_amdgcn_s_memrealtime();
+        if (!writer || qid >= QUERY_CLOCK_MAX) return;
+        const uint64_t hw = static_cast<uint64_t>(__builtin_amdgcn_s_getreg((31 << 11) | 4)) |
+                            (static_cast<uint64_t>(__builtin_amdgcn_s_getreg((31 << 11) | 20)) << 32);
+        bs_query_clock[qid * 3 + 0] = t0;
+        bs_query_clock[qid * 3 + 1] = t1;
+        bs_query_clock[qid * 3 + 2] = hw;
+    }
+#else
+    __device__ __forceinline__ void start() {}
+    __device__ __forceinline__ void finish(uint64_t, bool) {}
+#endif
+};
+
 // Register budget per instance, matched to what the LDS slice allows anyway: RaBitQ beams
 // up to 256 (about 7 KB of LDS per wavefront) are compiled for 5 wavefronts per SIMD (at most
 // 96 VGPRs); the loops with beams up to 256 and two passes of rows in flight (Bloom over rows
@@ -98,6 +126,8 @@ search_kernel(const SearchParams p) {
     if (pos >= p.nq) return;
     const uint64_t qid = p.qmap ? uniform(p.qmap[pos]) : pos;
     if (qid >= p.nq) return;
+    QueryClock qclk;
+    qclk.start();
 
     char* my = smem + static_cast<size_t>(coop > 1 ? 0u : wave) * p.lds_wave;
     uint64_t* scratch = reinterpret_cast<uint64_t*>(my + p.off_scratch);
@@ -524,6 +554,7 @@ search_kernel(const SearchParams p) {
         clk.flush(n_exp, n_iter);
     }
 
+    qclk.finish(qid, lane == 0 && (coop <= 1 || wave == 0));
     if (p.per_query && lane == 0) {
         uint32_t* pq = p.per_query + qid * 5;
         pq[0] = n_iter;

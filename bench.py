@@ -92,6 +92,9 @@ def parse():
                          "reference builder, src/build_rabitq.cpp:258)")
     ap.add_argument("--query-order", type=int, default=1, choices=(0, 1, 2),
                     help="bs_index_set_query_order: 0 off, 1 on from 4096 queries (the library default), 2 always")
+    ap.add_argument("--query-timeline", action="store_true",
+                    help="one launch of the clock build (libbs_hip_phase.so) with each query's start and end: "
+                         "resident wavefronts over time, the drain, per-XCD end times (base instances)")
     ap.add_argument("--phase-clocks", action="store_true",
                     help="rabitq: per-phase clocks of the search loop from the instrumented library "
                          "(make -C beam_search_collab_amd/csrc phase); one launch per --sweep topk (or --topk) "
@@ -499,6 +502,69 @@ def phase_clocks(args, g, q_t, cfg_for):
                       "points": out}), flush=True)
 
 
+def query_timeline(args, g, q_t, cfg_for):
+    """one base-mode launch of the clock build (libbs_hip_phase.so: each query's start and end by
+    s_memrealtime, one 100 MHz counter for the whole device, and the hardware id of its
+    wavefront): resident wavefronts over time, the drain after the last query starts, per-XCD
+    work and end times, wavefronts per CU"""
+    import collections
+    import ctypes as C
+    import numpy as np
+    import torch
+    import beam_search_collab_amd._lib as bl
+    read = bl.hip().bs_query_clock_read
+    read.argtypes = [C.c_void_p, C.c_uint64]
+    nq = q_t.shape[0]
+    assert nq <= 65536, "--query-timeline records up to 65536 queries"
+    cfg = cfg_for(args.mode, args.topk)
+    res = torch.empty((nq, args.K), dtype=torch.int32, device=q_t.device)
+    pq = torch.zeros((nq, 5), dtype=torch.int32, device=q_t.device)
+    for _ in range(max(args.warmup, 1)):
+        g.search_device(q_t.data_ptr(), nq, res.data_ptr(), args.K, args.mode, cfg, sync=True)
+    st = g.search_device(q_t.data_ptr(), nq, res.data_ptr(), args.K, args.mode, cfg, d_per_query=pq.data_ptr(),
+                         sync=True)
+    clk = np.zeros(nq * 3, np.uint64)
+    assert read(clk.ctypes.data, nq) == 0
+    clk = clk.reshape(nq, 3).astype(np.int64)
+    t0 = clk[:, 0].min()
+    beg, end, hw = clk[:, 0] - t0, clk[:, 1] - t0, clk[:, 2]
+    us = 0.01  # s_memrealtime ticks (10 ns) -> us
+    span = int(end.max())
+    dur = (end - beg).astype(np.float64)
+    xcc = (hw >> 32) & 0xF
+    cu = xcc * 1000 + ((hw >> 13) & 7) * 100 + ((hw >> 12) & 1) * 50 + ((hw >> 8) & 0xF)
+    pts = np.linspace(0, span, 21)[:-1] + span / 40
+    conc = [int(((beg <= t) & (end > t)).sum()) for t in pts]
+    per_cu = collections.Counter()
+    for t in pts[2:12]:  # the full part of the launch
+        run = (beg <= t) & (end > t)
+        per_cu.update(collections.Counter(cu[run].tolist()).values())
+    last = int(beg.max())
+    peak = max(conc)
+    row = {"mode": args.mode, "topk_size": args.topk, "K": args.K, "queries": nq,
+           "query_order": args.query_order, "launch_ms_instrumented": round(st["kernel_ms"], 3),
+           "span_us": round(span * us, 1), "last_start_us": round(last * us, 1),
+           "drain_after_last_start_us": round((span - last) * us, 1),
+           "running_at_last_start": int(((beg <= last) & (end > last)).sum()),
+           "idle_share_of_peak_slots": round(1.0 - float(dur.sum()) / (peak * span), 4),
+           "query_us": {"p50": round(float(np.percentile(dur, 50)) * us, 1),
+                        "p90": round(float(np.percentile(dur, 90)) * us, 1),
+                        "max": round(float(dur.max()) * us, 1), "cv": round(float(dur.std() / dur.mean()), 4)},
+           "resident_wavefronts_at_5pct_steps": conc, "peak_resident": peak,
+           "cus_seen": int(len(set(cu.tolist()))),
+           "wavefronts_per_cu_histogram": {str(k): v for k, v in sorted(per_cu.items())},
+           "xcd": [{"xcd": x, "queries": int((xcc == x).sum()),
+                    "busy_us": round(float(dur[xcc == x].sum()) * us, 1),
+                    "last_start_us": round(float(beg[xcc == x].max()) * us, 1),
+                    "end_us": round(float(end[xcc == x].max()) * us, 1)} for x in sorted(set(xcc.tolist()))],
+           "expansions_per_query": round(float(pq[:, 1].float().mean()), 2)}
+    log(f"{args.mode} topk {args.topk}: span {span * us:.0f} us, last start {last * us:.0f} us, drain "
+        f"{(span - last) * us:.0f} us, peak {peak} wavefronts on {row['cus_seen']} CUs, idle share "
+        f"{row['idle_share_of_peak_slots']:.3f}")
+    print(json.dumps({"metric": "per-query start/end clocks of one launch (s_memrealtime, clock build)",
+                      "config": {"workload": f"config {args.config}", "nq": nq}, "timeline": row}), flush=True)
+
+
 def main():
     args = parse()
     if args.traffic_child:
@@ -511,10 +577,11 @@ def main():
         sys.exit(2)
     import numpy as np
     import torch
-    if args.phase_clocks:
+    if args.phase_clocks or args.query_timeline:
         import beam_search_collab_amd._lib as _bl
         _bl.HIP_LIB_PATH = os.path.join(ROOT, "beam_search_collab_amd", "libbs_hip_phase.so")
-        assert args.mode == "rabitq", "--phase-clocks times the rabitq loop (--config C)"
+        assert not args.phase_clocks or args.mode == "rabitq", "--phase-clocks times the rabitq loop (--config C)"
+        assert not args.query_timeline or args.mode != "rabitq", "--query-timeline records the base instances"
     from beam_search_collab_amd import host, search
 
     assert torch.cuda.is_available(), "bench.py needs the GPU"
@@ -591,6 +658,9 @@ def main():
     stream = torch.cuda.current_stream().cuda_stream
     if args.phase_clocks:
         phase_clocks(args, g, q_t, cfg_for)
+        return
+    if args.query_timeline:
+        query_timeline(args, g, q_t, cfg_for)
         return
 
     def measure(mode, topk, k, steps, warmup):
