@@ -70,6 +70,16 @@ static hipError_t launch_any(const SearchParams& p, int TR, int CR, int PB, dim3
 
 #if BS_INST_MODE == 0
 #ifdef BS_PHASE_CLOCKS
+// the instrumented library's clock sums of the hash-filter (base, warp) instances
+// (PhaseClock): out[0..16) as bs_phase_clock holds them; reset != 0 clears them afterwards
+extern "C" int bs_phase_read_base(unsigned long long* out, int reset) {
+    if (hipMemcpyFromSymbol(out, HIP_SYMBOL(bs_phase_clock), sizeof(unsigned long long) * 16) != hipSuccess) return 1;
+    if (reset) {
+        const unsigned long long z[16] = {};
+        if (hipMemcpyToSymbol(HIP_SYMBOL(bs_phase_clock), z, sizeof(z)) != hipSuccess) return 2;
+    }
+    return 0;
+}
 // the instrumented library's per-query clocks of the hash-filter (base, warp) instances
 // (QueryClock): out[3 q + 0..2] = start, end, hardware id of queries q < n (n <= 65536)
 extern "C" int bs_query_clock_read(unsigned long long* out, uint64_t n) {

@@ -42,11 +42,13 @@ struct SearchParams {
     L2Shape L;
 };
 
-// Per-phase clocks of the RaBitQ loop, compiled only into the instrumented library (make
-// phase: -DBS_PHASE_CLOCKS, libbs_hip_phase.so, read by bs_phase_read): s_memtime at the
-// phase boundaries, summed per query and added to bs_phase_clock at the query's end (slots
-// 0-5 the loop's phases, 6 the final flush, rerank and results, 8 expansions, 9 iterations,
-// 10 queries).  In the library itself every call below is empty.
+// Per-phase clocks of the RaBitQ and base loops, compiled only into the instrumented library
+// (make phase: -DBS_PHASE_CLOCKS, libbs_hip_phase.so, read by bs_phase_read for the RaBitQ
+// instances and bs_phase_read_base for the hash-filter ones, each translation unit holding
+// its own sums): s_memtime at the phase boundaries, summed per query and added to
+// bs_phase_clock at the query's end (slots 0-5 the loop's phases, 6 the final flush, rerank
+// and results, 8 expansions, 9 iterations, 10 queries).  In the library itself every call
+// below is empty.
 #ifdef BS_PHASE_CLOCKS
 static __device__ unsigned long long bs_phase_clock[16];
 #endif
@@ -205,6 +207,8 @@ search_kernel(const SearchParams p) {
             }
         }
         int32_t until_reset = p.reset;
+        PhaseClock clk;  // instrumented build: 0 merge, 1 re-fill, 2 pick, 3 list + filter, 4 L2, 5 keys
+        clk.start();
         // The neighbour list of the predicted next parent is requested before the merge,
         // so its HBM round trip overlaps merge, refill and pick: after the merge the
         // smallest unexpanded key is the smaller of the beam's next unexpanded key and the
@@ -222,6 +226,7 @@ search_kernel(const SearchParams p) {
             if (any) beam_merge<TR, CR, (CR == 1)>(beam, ck, cm, T, scratch, merge_aux, st);
 #pragma unroll
             for (int rc = 0; rc < CR; ++rc) cm[rc] = 0;
+            clk.mark(0);
 
             // forgettable filter: clear and re-insert the beam ids (gpu_search_base.cuh:173-181)
             // in the reference's order, its descending buffer from position 0 (largest key
@@ -245,11 +250,13 @@ search_kernel(const SearchParams p) {
                     wave_sync();
                 }
             }
+            clk.mark(1);
 
             // pick the best unexpanded node
             const uint32_t parent = beam_pick<TR, false>(beam, st, &next_key);
             if (parent == INVALID) break;
             ++n_exp;
+            clk.mark(2);
 
             // expand: neighbours through the filter
             uint32_t child[CR], isnew[CR];
@@ -284,6 +291,7 @@ search_kernel(const SearchParams p) {
                 c += static_cast<uint32_t>(__builtin_popcountll(m));
             }
             wave_sync();
+            clk.mark(3);
             if (c == 0) continue;
             n_dist += c;
             if (coop > 1) {
@@ -295,6 +303,7 @@ search_kernel(const SearchParams p) {
             } else {
                 l2_rows<QMAX, PB>(q, vbase, vstride, cand_ids, cand_d, c, L);
             }
+            clk.mark(4);
 #pragma unroll
             for (int rc = 0; rc < CR; ++rc) {
                 const uint32_t j = static_cast<uint32_t>(rc) * 64u + lane;
@@ -316,7 +325,9 @@ search_kernel(const SearchParams p) {
                     }
                 }
             }
+            clk.mark(5);
         }
+        clk.mark(6);
         if (coop > 1) {  // release the helper wavefronts
             if (lane == 0) *batch = INVALID;
             __syncthreads();
@@ -338,6 +349,8 @@ search_kernel(const SearchParams p) {
                 if (dout) dout[e] = (beam[r] == EMPTY_KEY) ? FLT_MAX : key_dist(beam[r]);
             }
         }
+        clk.mark(6);
+        clk.flush(n_exp, n_iter);
     } else {
         // ---------------------------------------------------------------- rabitq
         HashLds hf;
