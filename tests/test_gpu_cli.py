@@ -38,10 +38,12 @@ def run_cli(cfg):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("mode", ["base", "warp2", "bwarp1", "rabitq"])
-def test_cli_matches_library(gpu, files, mode):
+@pytest.mark.parametrize("mode,topk", [("base", 128), ("warp2", 128), ("bwarp1", 128), ("rabitq", 128),
+                                       ("base", 2048), ("rabitq", 3000)])
+def test_cli_matches_library(gpu, files, mode, topk):
     f, ds = files
-    search_cfg = {"mode": mode, "K": 10, "topk_size": 128, "max_iterations": 1024}
+    cap = 8192 if topk > 1024 else 1024
+    search_cfg = {"mode": mode, "K": 10, "topk_size": topk, "max_iterations": 1024, "filter_capacity": cap}
     rc, out, err = run_cli({"data": f, "search": search_cfg})
     assert rc == 0, err
     lines = out.splitlines()
@@ -52,9 +54,9 @@ def test_cli_matches_library(gpu, files, mode):
     g = search.GPUGraph(ds["base"], ds["edges"])
     if mode == "rabitq":
         g.attach_rabitq(*ds["rq"])
-        cfg = GPURabitqSearchCfg(128, 1024, ds["erq"], 1024)
+        cfg = GPURabitqSearchCfg(topk, cap, ds["erq"], 1024)
     else:
-        cfg = GPUBaseSearchCfg(128, 1024, host.entry_point(ds["base"]), 1024, 16)
+        cfg = GPUBaseSearchCfg(topk, cap, host.entry_point(ds["base"]), 1024, 16)
     ids, _, _ = g.search(ds["q"], 10, mode, cfg)
     rec_lib, _ = host.recall(ids, ds["gt"])
     assert abs(rec_cli - rec_lib) < 1e-6, (rec_cli, rec_lib)
