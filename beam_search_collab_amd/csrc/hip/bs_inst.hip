@@ -103,6 +103,13 @@ hipError_t launch_search_rabitq(const SearchParams& p, int TR, int CR, int PB, d
     return launch_any(p, TR, CR, PB, g, b, lds, s, occ);
 }
 #ifdef BS_PHASE_CLOCKS
+// the instrumented library's per-query clocks of the narrow-code RaBitQ instances
+// (QueryClock), as bs_query_clock_read gives them for the hash-filter ones
+extern "C" int bs_query_clock_read_rabitq(unsigned long long* out, uint64_t n) {
+    if (n > QUERY_CLOCK_MAX) return 2;
+    return hipMemcpyFromSymbol(out, HIP_SYMBOL(bs_query_clock), sizeof(unsigned long long) * 3 * n) == hipSuccess ? 0
+                                                                                                             : 1;
+}
 // the instrumented library's clock sums of the narrow-code RaBitQ instances (PhaseClock):
 // out[0..16) as bs_phase_clock holds them; reset != 0 clears them afterwards
 extern "C" int bs_phase_read(unsigned long long* out, int reset) {

@@ -511,7 +511,7 @@ def phase_clocks(args, g, q_t, cfg_for):
 
 
 def query_timeline(args, g, q_t, cfg_for):
-    """one base-mode launch of the clock build (libbs_hip_phase.so: each query's start and end by
+    """one base- or rabitq-mode launch of the clock build (libbs_hip_phase.so: each query's start and end by
     s_memrealtime, one 100 MHz counter for the whole device, and the hardware id of its
     wavefront): resident wavefronts over time, the drain after the last query starts, per-XCD
     work and end times, wavefronts per CU"""
@@ -520,7 +520,7 @@ def query_timeline(args, g, q_t, cfg_for):
     import numpy as np
     import torch
     import beam_search_collab_amd._lib as bl
-    read = bl.hip().bs_query_clock_read
+    read = bl.hip().bs_query_clock_read_rabitq if args.mode == "rabitq" else bl.hip().bs_query_clock_read
     read.argtypes = [C.c_void_p, C.c_uint64]
     nq = q_t.shape[0]
     assert nq <= 65536, "--query-timeline records up to 65536 queries"
@@ -589,7 +589,8 @@ def main():
         import beam_search_collab_amd._lib as _bl
         _bl.HIP_LIB_PATH = os.path.join(ROOT, "beam_search_collab_amd", "libbs_hip_phase.so")
         assert not args.phase_clocks or args.mode in ("rabitq", "base"), "--phase-clocks times the rabitq or base loop"
-        assert not args.query_timeline or args.mode != "rabitq", "--query-timeline records the base instances"
+        assert not args.query_timeline or args.mode in ("base", "rabitq"), \
+            "--query-timeline records the base and the narrow-code rabitq instances"
     from beam_search_collab_amd import host, search
 
     assert torch.cuda.is_available(), "bench.py needs the GPU"

@@ -278,12 +278,14 @@ int bs_debug_filter(int bloom, uint32_t capacity, const uint32_t* keys, uint32_t
                     uint32_t bsize, uint32_t* out_new, const uint32_t* qkeys, uint32_t nquery,
                     uint32_t* out_contains);
 
-/* The instrumented build (libbs_hip_phase.so, `make phase`; not this library) exports three
+/* The instrumented build (libbs_hip_phase.so, `make phase`; not this library) exports four
  * readers of its clocks besides every entry point above, for measurement only:
  *   int bs_phase_read(unsigned long long out[16], int reset);       RaBitQ loop phase sums
  *   int bs_phase_read_base(unsigned long long out[16], int reset);  base loop phase sums
  *   int bs_query_clock_read(unsigned long long* out, uint64_t n);   start, end, hardware id
  *                                                                   of queries 0..n-1 (<= 65536)
+ *   int bs_query_clock_read_rabitq(unsigned long long* out, uint64_t n);  the same, narrow-code
+ *                                                                   RaBitQ launches
  * Slots of the phase sums: 0-5 the loop's phases, 6 the end of the query, 8 expansions,
  * 9 iterations, 10 queries. */
 
