@@ -92,6 +92,7 @@ def parse():
                          "reference builder, src/build_rabitq.cpp:258)")
     ap.add_argument("--query-order", type=int, default=1, choices=(0, 1, 2),
                     help="bs_index_set_query_order: 0 off, 1 on from 4096 queries (the library default), 2 always")
+    ap.add_argument("--timeline-npz", default="", help="--query-timeline: also save the raw clocks (npz)")
     ap.add_argument("--query-timeline", action="store_true",
                     help="one launch of the clock build (libbs_hip_phase.so) with each query's start and end: "
                          "resident wavefronts over time, the drain, per-XCD end times (base instances)")
@@ -566,6 +567,9 @@ def query_timeline(args, g, q_t, cfg_for):
                     "last_start_us": round(float(beg[xcc == x].max()) * us, 1),
                     "end_us": round(float(end[xcc == x].max()) * us, 1)} for x in sorted(set(xcc.tolist()))],
            "expansions_per_query": round(float(pq[:, 1].float().mean()), 2)}
+    if args.timeline_npz:
+        np.savez(args.timeline_npz, start=beg, end=end, hw=hw, per_query=pq.cpu().numpy(),
+                 qmap=(np.argsort(beg, kind="stable")))
     log(f"{args.mode} topk {args.topk}: span {span * us:.0f} us, last start {last * us:.0f} us, drain "
         f"{(span - last) * us:.0f} us, peak {peak} wavefronts on {row['cus_seen']} CUs, idle share "
         f"{row['idle_share_of_peak_slots']:.3f}")
