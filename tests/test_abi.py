@@ -69,3 +69,18 @@ def test_argument_errors_before_any_device_call():
     assert lib.bs_build_vamana_device(vecs, 2, 4, 2, 8, 0.5, 1, out, 0) == -1
     assert b"alpha" in lib.bs_last_error()
     assert lib.bs_build_vamana_device(vecs, 0, 4, 2, 8, 1.2, 1, out, 0) == -1
+
+
+def test_instrumented_build_exports_the_library_and_its_clock_readers():
+    """libbs_hip_phase.so (bench.py --phase-clocks / --query-timeline) exports every entry point
+    of bs_hip.h plus the clock readers that the header names in a comment"""
+    path = os.path.join(ROOT, "beam_search_collab_amd", "libbs_hip_phase.so")
+    if not os.path.exists(path):
+        pytest.skip("the instrumented build is made by build() (make phase)")
+    lib = ctypes.CDLL(path)
+    names = declared("bs_hip.h") + ["bs_phase_read", "bs_phase_read_base", "bs_query_clock_read",
+                                    "bs_query_clock_read_rabitq"]
+    missing = [n for n in names if not hasattr(lib, n)]
+    assert not missing, missing
+    plain = ctypes.CDLL(_lib.HIP_LIB_PATH)
+    assert not hasattr(plain, "bs_phase_read") and not hasattr(plain, "bs_query_clock_read")
