@@ -1,8 +1,9 @@
 """Seeded random search configurations against the oracle: ids, distances and per-query
 counters bit-exact for every mode, over odd beam sizes (1..4096, not multiples of 64), K from
 1 to 100 (above the beam in rabitq mode), filter capacities from 8 to 8192, resets, iteration
-limits and graph shapes with one, two and four candidate registers and narrow and wide RaBitQ
-codes.  A configuration whose workgroup would exceed the device's LDS is refused with a
+limits, launches in query order and scheduled (query order mode 2: labels, per-XCD runs and,
+for RaBitQ, the pilot search even at 12 queries), and graph shapes with one, two and four
+candidate registers and narrow and wide RaBitQ codes.  A configuration whose workgroup would exceed the device's LDS is refused with a
 ValueError naming the limit, and counts as checked."""
 import functools
 
@@ -58,12 +59,14 @@ def cases():
         cap = CAPS[int(rng.integers(len(CAPS)))]
         reset = RESETS[int(rng.integers(len(RESETS)))]
         max_it = MAX_ITS[int(rng.integers(len(MAX_ITS)))]
-        out.append(pytest.param(shape, mode, topk, K, cap, reset, max_it, id=f"{i}-{mode}-t{topk}-R{shape[2]}"))
+        order = int(rng.integers(1, 3))
+        out.append(pytest.param(shape, mode, topk, K, cap, reset, max_it, order,
+                                id=f"{i}-{mode}-t{topk}-R{shape[2]}-o{order}"))
     return out
 
 
-@pytest.mark.parametrize("shape,mode,topk,K,cap,reset,max_it", cases())
-def test_random_config_matches_oracle(gpu, shape, mode, topk, K, cap, reset, max_it):
+@pytest.mark.parametrize("shape,mode,topk,K,cap,reset,max_it,order", cases())
+def test_random_config_matches_oracle(gpu, shape, mode, topk, K, cap, reset, max_it, order):
     ds = dataset(*shape)
     rq = mode == "rabitq"
     if rq:
@@ -73,12 +76,15 @@ def test_random_config_matches_oracle(gpu, shape, mode, topk, K, cap, reset, max
         cfg = GPUBaseSearchCfg(topk, cap, ds["entry"], max_it, reset)
         omode = po.BASE_BLOOM if mode.startswith("bwarp") else po.BASE_HASH
         entry, oreset = ds["entry"], reset
-    ctx = (shape, mode, topk, K, cap, reset, max_it)
+    ctx = (shape, mode, topk, K, cap, reset, max_it, order)
+    ds["g"].set_query_order(order)
     try:
         ids, d, st = ds["g"].search(ds["q"], K, mode, cfg, with_dists=True)
     except ValueError as e:
         assert "LDS" in str(e), (ctx, str(e))
         return
+    finally:
+        ds["g"].set_query_order(1)
     oids, od, ost = ds["oi"].search(ds["q"], K, omode, topk, entry, max_it, cap, oreset, po.L2_WAVE)
     assert np.array_equal(ids, oids), ctx
     assert d.tobytes() == od.tobytes(), ctx
