@@ -75,6 +75,7 @@ extern "C" int bs_debug_l2(bs_index idx, const float* queries, uint64_t nq, cons
     uint32_t dim = 0, degree = 0;
     int rc = bs_index_info(idx, &n, &dim, &degree, nullptr, nullptr);
     if (rc) return rc;
+    if (npairs && (!queries || !qi || !ni || !out)) return dfail(BS_EINVAL, "queries, qi, ni and out must be given");
     for (uint64_t i = 0; i < npairs; ++i)
         if (qi[i] >= nq || ni[i] >= n) return dfail(BS_EINVAL, "pair index out of range");
     if (npairs == 0) return BS_OK;
@@ -169,6 +170,8 @@ extern "C" int bs_debug_fastscan(const float* query, const float* signs, uint32_
     uint32_t pdim = 1;
     while (pdim < dim) pdim <<= 1;
     if (pdim < 32 || pdim > 2048) return dfail(BS_EINVAL, "padded dim must be in 32..2048");
+    if (!query || !signs || !codes_out || !scal_out || !sum_q_out || (nn && (!codes_nbr || !factors || !raw_out || !est_out)))
+        return dfail(BS_EINVAL, "null buffer");
     if (nn == 0 || nn > 128 || nn > degree) return dfail(BS_EINVAL, "need 1 <= nn <= min(128, degree)");
     const uint32_t wpp = pdim / 32;
     DevBuf<float> dq, ds, dfac, dscal, dest;
@@ -263,6 +266,7 @@ extern "C" int bs_debug_beam(uint32_t topk, const uint64_t* keys, uint32_t nbatc
                              int pick_run, uint32_t* picked, uint64_t* beam_out) try {
     if (topk == 0 || topk > 4096) return dfail(BS_EINVAL, "topk must be in 1..4096");
     if (bsize == 0 || bsize > 128) return dfail(BS_EINVAL, "bsize must be in 1..128");
+    if (!beam_out || (nbatch && !keys) || (nbatch && picks && !picked)) return dfail(BS_EINVAL, "null buffer");
     DevBuf<uint64_t> dk, db;
     DevBuf<uint32_t> dp;
     const size_t nk = static_cast<size_t>(nbatch) * bsize;
@@ -317,6 +321,7 @@ __global__ void __launch_bounds__(64) dbg_sort_kernel(const uint64_t* keys, uint
 extern "C" int bs_debug_sort(const uint64_t* keys, uint32_t n, uint64_t* out) try {
     if (n == 0) return BS_OK;
     if (n > 4096) return dfail(BS_EINVAL, "n must be <= 4096");
+    if (!keys || !out) return dfail(BS_EINVAL, "keys and out must be given");
     DevBuf<uint64_t> dk, dout;
     DTRY(dk.alloc(n));
     DTRY(dout.alloc(n));
@@ -341,6 +346,7 @@ extern "C" int bs_debug_sort(const uint64_t* keys, uint32_t n, uint64_t* out) tr
 extern "C" int bs_debug_cost_order(const float* signal, uint64_t n, uint32_t* qmap, uint32_t* bucket) try {
     if (n == 0) return BS_OK;
     if (n > (1u << 18)) return dfail(BS_EINVAL, "n must be <= 262144");
+    if (!signal || !qmap || !bucket) return dfail(BS_EINVAL, "signal, qmap and bucket must be given");
     DevBuf<uint32_t> key, map, hist, cursor;
     DTRY(key.alloc(n));
     DTRY(map.alloc(n));
@@ -371,6 +377,7 @@ extern "C" int bs_debug_label_order(const uint32_t* labels, const float* lcost, 
     if (n == 0) return BS_OK;
     if (n > 65536) return dfail(BS_EINVAL, "n must be <= 65536");
     if (g == 0 || g > 8 || X == 0 || X > bso::ORDER_MAX_X) return dfail(BS_EINVAL, "g must be in 1..8, X in 1..32");
+    if (!labels || !qmap) return dfail(BS_EINVAL, "labels and qmap must be given");
     for (uint64_t i = 0; i < n; ++i)
         if (labels[i] >= bso::ORDER_P) return dfail(BS_EINVAL, "labels must be < 256");
     DevBuf<uint32_t> key, map;
@@ -445,6 +452,7 @@ __global__ void __launch_bounds__(64) dbg_filter_kernel(int bloom, uint32_t bits
 extern "C" int bs_debug_filter(int bloom, uint32_t capacity, const uint32_t* keys, uint32_t nbatch, uint32_t bsize,
                                uint32_t* out_new, const uint32_t* qkeys, uint32_t nquery, uint32_t* out_contains) try {
     if (bsize == 0 || bsize > 64) return dfail(BS_EINVAL, "bsize must be in 1..64");
+    if ((nbatch && (!keys || !out_new)) || (nquery && (!qkeys || !out_contains))) return dfail(BS_EINVAL, "null buffer");
     uint32_t bits = 0;
     while ((1ull << bits) < capacity) ++bits;
     size_t lds;

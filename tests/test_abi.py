@@ -84,3 +84,21 @@ def test_instrumented_build_exports_the_library_and_its_clock_readers():
     assert not missing, missing
     plain = ctypes.CDLL(_lib.HIP_LIB_PATH)
     assert not hasattr(plain, "bs_phase_read") and not hasattr(plain, "bs_query_clock_read")
+
+
+def test_debug_entry_points_refuse_null_buffers_before_any_device_call():
+    """the primitive entry points check their host buffers before touching the device"""
+    C = ctypes
+    lib = _lib.hip()
+    keys = (C.c_uint64 * 4)()
+    assert lib.bs_debug_sort(None, 4, keys) == -1
+    assert lib.bs_debug_sort(keys, 4, None) == -1
+    assert lib.bs_debug_beam(64, None, 1, 4, 1, 0, None, keys) == -1
+    assert lib.bs_debug_beam(64, keys, 1, 4, 0, 0, None, None) == -1
+    sig = (C.c_float * 4)()
+    assert lib.bs_debug_cost_order(sig, 4, None, None) == -1
+    lab = (C.c_uint32 * 4)()
+    assert lib.bs_debug_label_order(None, None, 4, 1, 8, lab) == -1
+    assert lib.bs_debug_filter(0, 64, None, 1, 4, lab, None, 0, None) == -1
+    assert lib.bs_debug_fastscan(None, sig, 32, 1, None, None, 0, 32, 0.0, None, None, None, None, None) == -1
+    assert b"null" in lib.bs_last_error() or b"must be given" in lib.bs_last_error()
