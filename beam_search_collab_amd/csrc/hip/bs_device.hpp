@@ -627,6 +627,7 @@ __device__ __forceinline__ void bitonic_sort(uint64_t (&v)[TR]) {
 // of the network makes its 32 TR compare-exchanges 64 at a time, and the keys come back.
 template <int TR>
 __device__ __forceinline__ void sort_beam_lds(uint64_t (&v)[TR], uint64_t* S) {
+    static_assert((TR & (TR - 1)) == 0, "the bitonic network sorts a power of two of keys");
     const uint32_t lane = lane_id();
     constexpr uint32_t N = 64u * TR;
 #pragma unroll
@@ -663,7 +664,8 @@ __device__ __forceinline__ void sort_beam(uint64_t (&v)[TR], uint64_t* S) {
     } else if constexpr ((TR & (TR - 1)) == 0) {
         bitonic_sort<TR>(v);
     } else {
-        constexpr int P = 16;
+        constexpr int P = 16;  // the register counts that are not a power of two: 10 and 12
+        static_assert(TR < P, "padded to 16 registers");
         uint64_t w[P];
 #pragma unroll
         for (int r = 0; r < P; ++r) w[r] = r < TR ? v[r] : EMPTY_KEY;
