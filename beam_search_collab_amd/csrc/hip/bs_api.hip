@@ -427,8 +427,10 @@ int make_plan(bs_index ix, const bs_search_cfg* cfg, uint64_t nq, Plan& pl) {
           : (T <= 640 && mode == BS_RABITQ) ? 10 : (T <= 768 && mode == BS_RABITQ) ? 12
           : T <= 1024 ? 16 : T <= 2048 ? 32 : 64;
     pl.CR = ix->degree <= 64 ? 1 : ix->degree <= 128 ? 2 : 4;
-    bsd::L2Shape L = bsd::l2_shape(ix->dim);
-    if (L.QR > 4) return fail(BS_EINVAL, "dim too large");
+    // RaBitQ with narrow codes (dim <= 128): one chunk per lane (bsd::l2_shape_lanes)
+    const bool narrow_rq = mode == BS_RABITQ && ix->wpp <= 4;
+    bsd::L2Shape L = narrow_rq ? bsd::l2_shape_lanes(ix->dim) : bsd::l2_shape(ix->dim);
+    if (L.QR > (narrow_rq ? 1u : 4u)) return fail(BS_EINVAL, "dim too large");
     // 32 rows per batch for the hash-filter loop over rows of up to 128 dims: 1M x 128,
     // degree 32: topk 256 4.58 -> 4.49 ms, topk 128 2.54 -> 2.39, topk 512 9.75 -> 8.66
     // (with the larger visit filter below); the Bloom loop keeps 16 (its wavefronts per CU

@@ -938,6 +938,24 @@ __host__ __device__ inline L2Shape l2_shape(uint32_t dim) {
     return L;
 }
 
+// The shape with one chunk per lane: G = pow2ceil(chunks) lanes per row (at most 64), so
+// QR = 1 for rows of up to 256 dims.  Used by the RaBitQ search with narrow codes (dim <= 128),
+// whose loop computes one row at a time (the parent's exact distance): the whole wavefront on
+// one row takes a quarter of the instructions of the 4-chunk shape, whose 8 lane groups would
+// each repeat the same row.  (orc_l2_wave_lanes in oracle/bs_oracle.c.)
+__host__ __device__ inline L2Shape l2_shape_lanes(uint32_t dim) {
+    L2Shape L;
+    L.chunks = (dim + 3) / 4;
+    uint32_t p = 1;
+    while (p < L.chunks) p <<= 1;
+    L.G = p > 64 ? 64 : p;
+    L.gshift = 0;
+    while ((1u << L.gshift) < L.G) ++L.gshift;
+    L.QR = (L.chunks + L.G - 1) / L.G;
+    L.rpp = 64 / L.G;
+    return L;
+}
+
 // Loads of PB rows (one row per lane group per pass), issued without waiting.  Every
 // load is unconditional -- chunks outside the row are redirected to chunk 0 of the same
 // row (l2_accum zeroes their difference) -- so all PB*QMAX loads of a lane are in flight

@@ -27,10 +27,11 @@ static hipError_t launch_one(const SearchParams& p, dim3 grid, dim3 block, size_
 template <int TR, int CR>
 static hipError_t launch_p(const SearchParams& p, int PB, dim3 g, dim3 b, size_t lds, hipStream_t s, int* occ) {
     // every dim <= 1024 fits 4 float4 chunks per lane (bsd::l2_shape).  Narrow RaBitQ codes
-    // mean dim <= 128, hence PB = 2; wide codes mean dim > 128, hence PB >= 4.
+    // mean dim <= 128, computed with one chunk per lane (bsd::l2_shape_lanes: 2-8 rows per
+    // pass), 8 passes in flight; wide codes mean dim > 128, hence PB >= 4.
     if constexpr (BS_INST_MODE == 2) {
         (void)PB;
-        return launch_one<TR, CR, 4, 2>(p, g, b, lds, s, occ);
+        return launch_one<TR, CR, 1, 8>(p, g, b, lds, s, occ);
     } else if constexpr (BS_INST_MODE == 3) {
         return PB == 4 ? launch_one<TR, CR, 4, 4>(p, g, b, lds, s, occ) : launch_one<TR, CR, 4, 8>(p, g, b, lds, s, occ);
     } else {

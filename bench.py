@@ -312,8 +312,9 @@ def cpu_baseline(files, nq_total, run, args):
 def kernel_name(mode, topk, degree, dim):
     """symbol of the search-kernel instance a launch uses (beam registers TR = topk/64 rounded
     up to 1, 2, 4, 8, 16, 32, 64, or 10 / 12 for rabitq beams of 513..640 / 641..768,
-    candidate registers CR = degree/64 rounded up to 1, 2, 4, 4 float4 chunks per lane, filter/mode id, row
-    passes in flight PB from the L2 row shape and the rows per batch)"""
+    candidate registers CR = degree/64 rounded up to 1, 2, 4, 4 float4 chunks per lane (1 for rabitq
+    with narrow codes, 8 passes), filter/mode id, row passes in flight PB from the L2 row shape and
+    the rows per batch)"""
     m = {"base": 0, "warp": 0, "bwarp": 1, "rabitq": 2}[mode.rstrip("0123456789")]
     tr = 1 if topk <= 64 else 2 if topk <= 128 else 4 if topk <= 256 else 8 if topk <= 512 else \
         10 if (topk <= 640 and m == 2) else 12 if (topk <= 768 and m == 2) else 16 if topk <= 1024 else \
@@ -328,6 +329,8 @@ def kernel_name(mode, topk, degree, dim):
     pb = min(max(rows // (64 // g), 2), 8)
     if m == 2 and dim > 128:
         m = 3  # rabitq with wide codes (pdim > 128)
+    elif m == 2:
+        return f"bsd::search_kernel<{tr}, {cr}, 1, 2, 8>"  # narrow codes: one chunk per lane
     return f"bsd::search_kernel<{tr}, {cr}, 4, {m}, {pb}>"
 
 

@@ -13,8 +13,10 @@
  *       committed under tests/golden/fastscan_*.bin; plus closed forms (raw sum is the
  *       integer sum of selected codes; codes follow the Sylvester-Hadamard rotation).
  *   orc_l2_seq       reference cpu_cli ids (bit-exact) through ORC_BASE_CPUREF.
- *   orc_l2_wave      fp64 sum within 1e-5 relative; exact on integer-valued inputs
- *                    (every partial sum is an exactly representable integer).
+ *   orc_l2_wave, orc_l2_wave_lanes
+ *                    fp64 sum within 1e-5 relative; exact on integer-valued inputs
+ *                    (every partial sum is an exactly representable integer); the two
+ *                    orders differ in the last bits (tests/test_oracle_semantics.py).
  *   ORC_BASE_CPUREF, ORC_RABITQ_CPUREF
  *                    result ids of the reference cpu_cli (oracle/_ref/cpu_cli) on
  *                    synthetic sets, committed under tests/golden/cpucli_*.npz.
@@ -112,10 +114,10 @@ void orc_l2_wave_shape(int dim, int* group, int* per_lane) {
     *per_lane = (chunks + g - 1) / g;
 }
 
-float orc_l2_wave(const float* a, const float* b, int dim) {
-    int G, QR;
-    orc_l2_wave_shape(dim, &G, &QR);
+/* the same order for a given lane count G per row (QR = ceil(chunks / G) chunks per lane) */
+static float l2_wave_g(const float* a, const float* b, int dim, int G) {
     int chunks = (dim + 3) / 4;
+    int QR = (chunks + G - 1) / G;
     float P[64], Q[64];
     for (int l = 0; l < G; ++l) {
         float p = 0.0f;
@@ -138,8 +140,31 @@ float orc_l2_wave(const float* a, const float* b, int dim) {
     return P[0];
 }
 
+float orc_l2_wave(const float* a, const float* b, int dim) {
+    int G, QR;
+    orc_l2_wave_shape(dim, &G, &QR);
+    return l2_wave_g(a, b, dim, G);
+}
+
+/* The one-chunk-per-lane form the RaBitQ search with narrow codes (padded dim <= 128) uses
+ * for every distance: G = pow2ceil(chunks) lanes (at most 64), one chunk each, the same
+ * butterfly over G lanes. */
+float orc_l2_wave_lanes(const float* a, const float* b, int dim) {
+    int chunks = (dim + 3) / 4;
+    int g = 1;
+    while (g < chunks) g <<= 1;
+    if (g > 64) g = 64;
+    return l2_wave_g(a, b, dim, g);
+}
+
 static float l2_of(int kind, const float* a, const float* b, int dim) {
     return kind == ORC_L2_SEQ ? orc_l2_seq(a, b, dim) : orc_l2_wave(a, b, dim);
+}
+
+/* the RaBitQ GPU search's distances: one chunk per lane with narrow codes (pdim <= 128) */
+static float l2_rq(int kind, int pdim, const float* a, const float* b, int dim) {
+    if (kind == ORC_L2_WAVE && pdim <= 128) return orc_l2_wave_lanes(a, b, dim);
+    return l2_of(kind, a, b, dim);
 }
 
 /* ------------------------------------------------------------------------- */
@@ -686,7 +711,7 @@ static void search_rabitq_gpu(const orc_index* ix, const orc_cfg* cfg, const flo
     hash_init(&h, cfg->filter_capacity);
     uint64_t* cand = (uint64_t*)malloc(sizeof(uint64_t) * (size_t)(R > (int)b.T ? R : (int)b.T));
     const uint32_t ep = cfg->entry_point;
-    uint64_t e = orc_make_key(l2_of(cfg->l2_kind, q, ix->vecs + (size_t)ep * dim, dim), ep, 0);
+    uint64_t e = orc_make_key(l2_rq(cfg->l2_kind, pdim, q, ix->vecs + (size_t)ep * dim, dim), ep, 0);
     st->dist_evals++;
     beam_merge(&b, &e, 1);
     hashf seen; /* mutant 1 only */
@@ -699,7 +724,7 @@ static void search_rabitq_gpu(const orc_index* ix, const orc_cfg* cfg, const flo
         if (p == ORC_INVALID_ID) break;
         if (!hash_insert(&h, p) && !MUTANT(2)) continue;
         st->expansions++;
-        float exact = l2_of(cfg->l2_kind, q, ix->vecs + (size_t)p * dim, dim);
+        float exact = l2_rq(cfg->l2_kind, pdim, q, ix->vecs + (size_t)p * dim, dim);
         st->dist_evals++;
         const uint32_t* row = ix->edges + (size_t)p * R;
         const uint32_t* pc = ix->codes + (size_t)p * R * wpp;
@@ -722,7 +747,7 @@ static void search_rabitq_gpu(const orc_index* ix, const orc_cfg* cfg, const flo
     for (uint32_t i = 0; i < b.T; ++i) {
         if (b.k[i] == ORC_EMPTY_KEY) continue;
         uint32_t id = key_id(b.k[i]);
-        cand[nv++] = orc_make_key(l2_of(cfg->l2_kind, q, ix->vecs + (size_t)id * dim, dim), id, 0);
+        cand[nv++] = orc_make_key(l2_rq(cfg->l2_kind, pdim, q, ix->vecs + (size_t)id * dim, dim), id, 0);
         st->rerank_evals++;
     }
     qsort(cand, nv, sizeof(uint64_t), cmp_u64);

@@ -84,6 +84,7 @@ uint64_t orc_make_key(float dist, uint32_t id, int expanded);
 /* ---- L2 ---- */
 float orc_l2_seq(const float* a, const float* b, int dim);
 float orc_l2_wave(const float* a, const float* b, int dim);
+float orc_l2_wave_lanes(const float* a, const float* b, int dim);
 void orc_l2_wave_shape(int dim, int* group, int* per_lane);
 
 /* ---- fastscan (fastscan.cuh; unittest/test_fastscan.cu:54-145) ---- */

@@ -53,6 +53,7 @@ def lib():
             "orc_make_key": (u64, [f32, u32, C.c_int]),
             "orc_l2_seq": (f32, [vp, vp, C.c_int]),
             "orc_l2_wave": (f32, [vp, vp, C.c_int]),
+            "orc_l2_wave_lanes": (f32, [vp, vp, C.c_int]),
             "orc_padded_dim": (C.c_int, [C.c_int]),
             "orc_dither_hash": (u32, [u32, u32]),
             "orc_quantize_dither": (None, [vp, vp, C.c_int, u32, vp, vp, vp, vp]),
@@ -103,6 +104,12 @@ def l2_wave(a, b):
     a = np.ascontiguousarray(a, np.float32)
     b = np.ascontiguousarray(b, np.float32)
     return lib().orc_l2_wave(_p(a), _p(b), a.shape[0])
+
+
+def l2_wave_lanes(a, b):
+    a = np.ascontiguousarray(a, np.float32)
+    b = np.ascontiguousarray(b, np.float32)
+    return lib().orc_l2_wave_lanes(_p(a), _p(b), a.shape[0])
 
 
 def l2_seq(a, b):

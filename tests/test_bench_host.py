@@ -20,7 +20,7 @@ def test_kernel_name_matches_instance_rules():
     # TR = topk/64 (1,2,4,8), CR = degree/64 (1, 2, 4), PB from the row shape and the rows per
     # batch (32 rows for the hash loop over rows of up to 128 dims: 4 passes of 8; 16 rows
     # otherwise: 2 up to dim 128, 4 up to 256, 8 above), rabitq with pdim > 128 uses the
-    # wide instance (mode 3)
+    # wide instance (mode 3), rabitq with narrow codes one chunk per lane (QMAX 1, 8 passes)
     assert bench.kernel_name("base", 256, 32, 128) == "bsd::search_kernel<4, 1, 4, 0, 4>"
     assert bench.kernel_name("warp2", 64, 100, 100) == "bsd::search_kernel<1, 2, 4, 0, 4>"
     assert bench.kernel_name("warp1", 64, 200, 100) == "bsd::search_kernel<1, 4, 4, 0, 4>"
@@ -28,10 +28,10 @@ def test_kernel_name_matches_instance_rules():
     assert bench.kernel_name("bwarp1", 128, 64, 200) == "bsd::search_kernel<2, 1, 4, 1, 4>"
     assert bench.kernel_name("base", 256, 32, 200) == "bsd::search_kernel<4, 1, 4, 0, 4>"
     assert bench.kernel_name("base", 512, 32, 960) == "bsd::search_kernel<8, 1, 4, 0, 8>"
-    assert bench.kernel_name("rabitq", 256, 32, 128) == "bsd::search_kernel<4, 1, 4, 2, 2>"
+    assert bench.kernel_name("rabitq", 256, 32, 128) == "bsd::search_kernel<4, 1, 1, 2, 8>"
     assert bench.kernel_name("rabitq", 256, 32, 960) == "bsd::search_kernel<4, 1, 4, 3, 8>"
     # rabitq beams of 513..768 have a 12-register instance; the other modes use 16
-    assert bench.kernel_name("rabitq", 768, 32, 128) == "bsd::search_kernel<12, 1, 4, 2, 2>"
+    assert bench.kernel_name("rabitq", 768, 32, 128) == "bsd::search_kernel<12, 1, 1, 2, 8>"
     assert bench.kernel_name("base", 768, 32, 128) == "bsd::search_kernel<16, 1, 4, 0, 4>"
 
 

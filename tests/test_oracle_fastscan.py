@@ -79,18 +79,29 @@ def test_dither_hash_is_the_reference_mixer():
 
 
 def test_l2_orders_against_fp64_and_integers():
-    """orc_l2_wave (the kernels' lane order) and orc_l2_seq (the reference CPU's sequential
-    sum): within 1e-5 relative of an fp64 sum, and exact when every partial sum is an
-    integer below 2^24 (then every order gives the same float)"""
+    """orc_l2_wave (the kernels' lane order), orc_l2_wave_lanes (its one-chunk-per-lane form,
+    the RaBitQ search with narrow codes) and orc_l2_seq (the reference CPU's sequential sum):
+    within 1e-5 relative of an fp64 sum, and exact when every partial sum is an integer below
+    2^24 (then every order gives the same float); the two lane orders are different orders
+    (they differ in the last bits on some inputs of more than 4 dims)"""
     rng = np.random.default_rng(4)
+    differ = 0
     for dim in (1, 3, 16, 25, 32, 100, 128, 200, 384, 960, 1024):
         for _ in range(20):
             a = rng.standard_normal(dim).astype(np.float32) * 10
             b = rng.standard_normal(dim).astype(np.float32) * 10
             want = float(((a.astype(np.float64) - b.astype(np.float64)) ** 2).sum())
             assert abs(po.l2_wave(a, b) - want) <= 1e-5 * want
+            assert abs(po.l2_wave_lanes(a, b) - want) <= 1e-5 * want
             assert abs(po.l2_seq(a, b) - want) <= 1e-5 * want
+            differ += po.l2_wave(a, b) != po.l2_wave_lanes(a, b)
             ai = rng.integers(0, 16, dim).astype(np.float32)
             bi = rng.integers(0, 16, dim).astype(np.float32)
             exact = int(((ai.astype(np.int64) - bi.astype(np.int64)) ** 2).sum())
             assert po.l2_wave(ai, bi) == exact and po.l2_seq(ai, bi) == exact
+            assert po.l2_wave_lanes(ai, bi) == exact
+        if dim <= 4:  # one chunk: both forms are the same sum
+            assert all(po.l2_wave(x, y) == po.l2_wave_lanes(x, y)
+                       for x, y in ((rng.standard_normal(dim).astype(np.float32),
+                                     rng.standard_normal(dim).astype(np.float32)) for _ in range(5)))
+    assert differ > 20
