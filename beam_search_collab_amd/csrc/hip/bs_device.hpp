@@ -939,10 +939,11 @@ __host__ __device__ inline L2Shape l2_shape(uint32_t dim) {
 }
 
 // The shape with one chunk per lane: G = pow2ceil(chunks) lanes per row (at most 64), so
-// QR = 1 for rows of up to 256 dims.  Used by the RaBitQ search with narrow codes (dim <= 128),
-// whose loop computes one row at a time (the parent's exact distance): the whole wavefront on
-// one row takes a quarter of the instructions of the 4-chunk shape, whose 8 lane groups would
-// each repeat the same row.  (orc_l2_wave_lanes in oracle/bs_oracle.c.)
+// QR = 1 for rows of up to 256 dims.  Used by the RaBitQ search with narrow codes (dim <= 128)
+// in its loop, which computes one row at a time (the entry point, then each expanded node's
+// exact distance): the whole wavefront on one row takes a quarter of the instructions of the
+// 4-chunk shape, whose 8 lane groups would each repeat the same row.  Its final rerank of many
+// rows keeps the 4-chunk shape.  (orc_l2_wave_lanes in oracle/bs_oracle.c.)
 __host__ __device__ inline L2Shape l2_shape_lanes(uint32_t dim) {
     L2Shape L;
     L.chunks = (dim + 3) / 4;

@@ -520,7 +520,17 @@ search_kernel(const SearchParams p) {
         }
         wave_sync();
         // the valid entries are the first nvb (the beam is sorted, empty keys last)
-        l2_rows<QMAX, PB>(q, rbase, rstride, ids, rd, nvb, L);
+        if constexpr (QMAX == 1) {
+            // narrow codes: the loop's one-chunk-per-lane rows fit one row per pass per 32
+            // lanes; the rerank's many rows go 4 chunks per lane (8 rows of 128 dims per pass,
+            // the base search's order), with the query reloaded in that layout
+            const L2Shape L4 = l2_shape(p.dim);
+            float4 q4[4];
+            load_query<4>(qv, p.dim, lane & (L4.G - 1), L4, q4);
+            l2_rows<4, 2>(q4, rbase, rstride, ids, rd, nvb, L4);
+        } else {
+            l2_rows<QMAX, PB>(q, rbase, rstride, ids, rd, nvb, L);
+        }
         n_rr += nvb;
 #pragma unroll
         for (int r = 0; r < TR; ++r) {

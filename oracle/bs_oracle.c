@@ -147,7 +147,8 @@ float orc_l2_wave(const float* a, const float* b, int dim) {
 }
 
 /* The one-chunk-per-lane form the RaBitQ search with narrow codes (padded dim <= 128) uses
- * for every distance: G = pow2ceil(chunks) lanes (at most 64), one chunk each, the same
+ * for the distances of its loop (the entry point and each expanded node; the final rerank
+ * keeps orc_l2_wave): G = pow2ceil(chunks) lanes (at most 64), one chunk each, the same
  * butterfly over G lanes. */
 float orc_l2_wave_lanes(const float* a, const float* b, int dim) {
     int chunks = (dim + 3) / 4;
@@ -161,7 +162,7 @@ static float l2_of(int kind, const float* a, const float* b, int dim) {
     return kind == ORC_L2_SEQ ? orc_l2_seq(a, b, dim) : orc_l2_wave(a, b, dim);
 }
 
-/* the RaBitQ GPU search's distances: one chunk per lane with narrow codes (pdim <= 128) */
+/* the RaBitQ GPU search's loop distances: one chunk per lane with narrow codes (pdim <= 128) */
 static float l2_rq(int kind, int pdim, const float* a, const float* b, int dim) {
     if (kind == ORC_L2_WAVE && pdim <= 128) return orc_l2_wave_lanes(a, b, dim);
     return l2_of(kind, a, b, dim);
@@ -747,7 +748,7 @@ static void search_rabitq_gpu(const orc_index* ix, const orc_cfg* cfg, const flo
     for (uint32_t i = 0; i < b.T; ++i) {
         if (b.k[i] == ORC_EMPTY_KEY) continue;
         uint32_t id = key_id(b.k[i]);
-        cand[nv++] = orc_make_key(l2_rq(cfg->l2_kind, pdim, q, ix->vecs + (size_t)id * dim, dim), id, 0);
+        cand[nv++] = orc_make_key(l2_of(cfg->l2_kind, q, ix->vecs + (size_t)id * dim, dim), id, 0);
         st->rerank_evals++;
     }
     qsort(cand, nv, sizeof(uint64_t), cmp_u64);

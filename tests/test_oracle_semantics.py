@@ -80,9 +80,9 @@ def test_rabitq_gpu_semantics_properties(golden_sets, name):
         cids, _, _ = oi.search(q, 10, po.RABITQ_CPUREF, topk, ep, 1024, 1024, 0, po.L2_SEQ)
         for i in range(q.shape[0]):
             valid = ids[i] != po.INVALID_ID
-            # exact-L2 rerank (one chunk per lane: narrow codes), ascending, deduplicated
+            # exact-L2 rerank (the kernels' 4-chunk order), ascending, deduplicated
             for j in np.nonzero(valid)[0]:
-                assert d[i, j] == np.float32(po.l2_wave_lanes(q[i], base[ids[i, j]]))
+                assert d[i, j] == np.float32(po.l2_wave(q[i], base[ids[i, j]]))
             assert np.all(np.diff(d[i][valid]) >= 0)
             assert len(set(ids[i][valid].tolist())) == int(valid.sum())
         assert np.all(st[:, 4] > 0)  # rerank evaluations
