@@ -497,8 +497,16 @@ __device__ __forceinline__ uint32_t pending_pick(uint64_t (&beam)[TR], BeamState
     uint32_t at;
     uint64_t mp;
     const uint64_t ub = beam_peek<TR>(beam, st, at, mp);
-    // the list's smallest unmarked key
-    const uint64_t pmin = pd.n > 0 ? wave_min64((v & 1ull) ? EMPTY_KEY : v) : EMPTY_KEY;
+    // the list's smallest unmarked key, wanted only when it is <= ub: the lanes whose
+    // unmarked key is <= ub say whether it is, and with one such lane the key is its key
+    // (1M x 128, 10k queries, rabitq topk 512 3.72 -> 3.66 ms, 768 5.88 -> 5.84)
+    uint64_t pmin = EMPTY_KEY;
+    if (pd.n > 0) {
+        const uint64_t um = (v & 1ull) ? EMPTY_KEY : v;
+        const uint64_t le = ballot(um <= ub && um != EMPTY_KEY);
+        if (le != 0)
+            pmin = (le & (le - 1u)) == 0 ? readlane64(um, static_cast<uint32_t>(__builtin_ctzll(le))) : wave_min64(um);
+    }
     const bool from_list = pmin <= ub && pmin != EMPTY_KEY;
     const uint64_t u = from_list ? pmin : ub;
     if (u == EMPTY_KEY) return INVALID;
