@@ -391,8 +391,8 @@ __device__ __forceinline__ uint64_t wave_min64(uint64_t v) {
     uint32_t h = vh;
     h = min(h, bsw::xor_lane<1>(h));
     h = min(h, bsw::xor_lane<2>(h));
-    h = min(h, bsw::xor_lane<4>(h));
-    h = min(h, bsw::xor_lane<8>(h));
+    h = min(h, bsw::partner<4>(h));
+    h = min(h, bsw::partner<8>(h));
     const uint32_t m = min(min(readlane(h, 0), readlane(h, 16)), min(readlane(h, 32), readlane(h, 48)));
     const uint64_t at = ballot(vh == m);
     const uint32_t l0 = static_cast<uint32_t>(__builtin_ctzll(at));
@@ -400,8 +400,8 @@ __device__ __forceinline__ uint64_t wave_min64(uint64_t v) {
     uint32_t lo = bsw::lane_in(at) ? static_cast<uint32_t>(v) : 0xFFFFFFFFu;
     lo = min(lo, bsw::xor_lane<1>(lo));
     lo = min(lo, bsw::xor_lane<2>(lo));
-    lo = min(lo, bsw::xor_lane<4>(lo));
-    lo = min(lo, bsw::xor_lane<8>(lo));
+    lo = min(lo, bsw::partner<4>(lo));
+    lo = min(lo, bsw::partner<8>(lo));
     const uint32_t ml = min(min(readlane(lo, 0), readlane(lo, 16)), min(readlane(lo, 32), readlane(lo, 48)));
     return (static_cast<uint64_t>(m) << 32) | ml;
 }
@@ -579,8 +579,8 @@ __device__ __forceinline__ uint64_t wave_min_key(const uint64_t (&k)[CR]) {
     uint32_t h = vh;
     h = min(h, bsw::xor_lane<1>(h));
     h = min(h, bsw::xor_lane<2>(h));
-    h = min(h, bsw::xor_lane<4>(h));
-    h = min(h, bsw::xor_lane<8>(h));
+    h = min(h, bsw::partner<4>(h));
+    h = min(h, bsw::partner<8>(h));
     const uint32_t m = min(min(readlane(h, 0), readlane(h, 16)), min(readlane(h, 32), readlane(h, 48)));
     return readlane64(v, static_cast<uint32_t>(__builtin_ctzll(ballot(vh == m))));
 }
@@ -1265,14 +1265,15 @@ __device__ __forceinline__ uint32_t raw_halves(const uint32_t* planes4, const Co
             n += static_cast<uint32_t>(__builtin_popcount(w[b].y & c.y));
             r += n << b;
         }
-        return r + bsw::xor_lane<32>(r);
+        return r;
     };
-    uint32_t raw = half_sum(h.a);
-    if (R > 32u) {
-        const uint32_t rb = half_sum(h.b);
-        raw = lane < 32u ? raw : rb;
-    }
-    return raw;
+    // v_permlane32_swap(a, b) leaves (a's lower half, b's lower half) in result 0 and (a's
+    // upper half, b's upper half) in result 1: their sum holds neighbour l's two halves in
+    // lane l < 32 and neighbour 32 + (l - 32)'s in lane l >= 32
+    const uint32_t ra = half_sum(h.a);
+    const uint32_t rb = R > 32u ? half_sum(h.b) : ra;
+    const auto r = __builtin_amdgcn_permlane32_swap(ra, rb, false, false);
+    return r[0] + r[1];
 }
 
 // raw = sum_b 2^b * popcount(plane_b & code) over the four words of a quad

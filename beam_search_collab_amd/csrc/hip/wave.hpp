@@ -111,6 +111,22 @@ __device__ __forceinline__ uint64_t xor_lane64_rt(uint64_t v, uint32_t s) {
     }
 }
 
+// Exchanges of a butterfly reduction.  Once every aligned group of S lanes holds one value
+// (the reduction's earlier steps made it so), any lane of the partner group will do: at
+// distances 4 and 8 one DPP mirror reaches the other quad / half-row (xor_lane needs two),
+// and at 16 and 32 one lane swap leaves the pair's two values in the two results in every
+// lane, so no select is needed (op(r[0], r[1]) is the pair's result).  The results are the
+// xor butterfly's bit for bit as long as op is commutative.
+template <int S>
+__device__ __forceinline__ uint32_t partner(uint32_t v) {
+    static_assert(S == 4 || S == 8, "mirror partners exist at distances 4 and 8");
+    return S == 4 ? dpp<DPP_HALF_MIRROR>(v) : dpp<DPP_MIRROR>(v);
+}
+template <int S>
+__device__ __forceinline__ float partner_f(float v) {
+    return __uint_as_float(partner<S>(__float_as_uint(v)));
+}
+
 // value of lane (this lane - 1); lane 0 gets lane 63's value
 __device__ __forceinline__ uint32_t prev_lane(uint32_t v) {
     return static_cast<uint32_t>(
@@ -118,25 +134,38 @@ __device__ __forceinline__ uint32_t prev_lane(uint32_t v) {
 }
 
 // Sum over aligned groups of G lanes (G a power of two <= 64) by an xor butterfly:
-// p_l += p_{l^s} for s = 1, 2, ..., G/2.  Every lane of a group ends with the same
-// value (float addition is commutative).  All 64 lanes must be active.
+// p_l += p_{l^s} for s = 1, 2, ..., G/2, the partners from 4 on taken by the reduction
+// exchanges above.  Every lane of a group ends with the same value (float addition is
+// commutative).  All 64 lanes must be active.
 __device__ __forceinline__ float group_sum(float p, uint32_t G) {
     if (G > 1) p = p + xor_lane_f<1>(p);
     if (G > 2) p = p + xor_lane_f<2>(p);
-    if (G > 4) p = p + xor_lane_f<4>(p);
-    if (G > 8) p = p + xor_lane_f<8>(p);
-    if (G > 16) p = p + xor_lane_f<16>(p);
-    if (G > 32) p = p + xor_lane_f<32>(p);
+    if (G > 4) p = p + partner_f<4>(p);
+    if (G > 8) p = p + partner_f<8>(p);
+    if (G > 16) {
+        const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(p), __float_as_uint(p), false, false);
+        p = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+    }
+    if (G > 32) {
+        const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(p), __float_as_uint(p), false, false);
+        p = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+    }
     return p;
 }
 
 __device__ __forceinline__ uint32_t group_sum_u32(uint32_t p, uint32_t G) {
     if (G > 1) p += xor_lane<1>(p);
     if (G > 2) p += xor_lane<2>(p);
-    if (G > 4) p += xor_lane<4>(p);
-    if (G > 8) p += xor_lane<8>(p);
-    if (G > 16) p += xor_lane<16>(p);
-    if (G > 32) p += xor_lane<32>(p);
+    if (G > 4) p += partner<4>(p);
+    if (G > 8) p += partner<8>(p);
+    if (G > 16) {
+        const auto r = __builtin_amdgcn_permlane16_swap(p, p, false, false);
+        p = r[0] + r[1];
+    }
+    if (G > 32) {
+        const auto r = __builtin_amdgcn_permlane32_swap(p, p, false, false);
+        p = r[0] + r[1];
+    }
     return p;
 }
 
