@@ -752,14 +752,21 @@ struct HashLds {
     // a mask, until each of them has met its key or an empty slot.  A key's sequence starts
     // at its home slot: the slots before it in its group of 4 are not in the sequence (they
     // end it, after a full turn).
+    // The first group (home_group, read ahead by the caller so that its LDS latency hides
+    // behind other work) is passed in.
+    __device__ __forceinline__ uint4 home_group(uint32_t k) const {
+        return reinterpret_cast<const uint4*>(t)[home(k) >> 2];
+    }
     __device__ __forceinline__ uint64_t contains_mask(uint32_t k, uint64_t active) const {
+        return contains_mask(k, active, home_group(k));
+    }
+    __device__ __forceinline__ uint64_t contains_mask(uint32_t k, uint64_t active, uint4 v) const {
         const uint4* t4 = reinterpret_cast<const uint4*>(t);
         const uint32_t s0 = home(k);
         const uint32_t nq = size >> 2;
         uint32_t q = s0 >> 2;
         const uint32_t f = s0 & 3u;
         const uint64_t f0 = ballot(f == 0u), f1 = ballot(f <= 1u), f2 = ballot(f <= 2u);
-        uint4 v = t4[q];
         uint64_t hit = (ballot(v.x == k) & f0) | (ballot(v.y == k) & f1) | (ballot(v.z == k) & f2) | ballot(v.w == k);
         const uint64_t emp = (ballot(v.x == INVALID) & f0) | (ballot(v.y == INVALID) & f1) |
                              (ballot(v.z == INVALID) & f2) | ballot(v.w == INVALID);

@@ -450,6 +450,11 @@ search_kernel(const SearchParams p) {
             if (!fresh_parent) continue;
             ++n_exp;
 
+            // the home groups of the neighbours' expanded-set sequences, read now so that the
+            // lookups below do not wait for the LDS (the parent's insert above is visible)
+            uint4 hg[CR];
+#pragma unroll
+            for (int rc = 0; rc < CR; ++rc) hg[rc] = hf.home_group(child[rc]);
             // exact distance of the parent
             float pe[1];
             l2_accum<QMAX, 1>(q, pv, lig, L, pe);
@@ -491,7 +496,7 @@ search_kernel(const SearchParams p) {
                 const uint64_t key = make_key(est, child[rc]);
                 const uint64_t below = ok & ballot(key < thr_k);
                 const uint64_t probe = count_all ? ok : below;
-                const uint64_t fresh = probe ? probe & ~hf.contains_mask(child[rc], probe) : 0ull;
+                const uint64_t fresh = probe ? probe & ~hf.contains_mask(child[rc], probe, hg[rc]) : 0ull;
                 ck[rc] = bsw::lane_in(below & fresh) ? key : EMPTY_KEY;
                 cm[rc] = below & fresh;
                 nv += static_cast<uint32_t>(__builtin_popcountll(fresh));
