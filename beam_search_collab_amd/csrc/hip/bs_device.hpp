@@ -439,24 +439,24 @@ __device__ __forceinline__ void pending_flush(uint64_t (&beam)[TR], PendingList&
     pd.v = EMPTY_KEY;
 }
 
-// candidates ck (lanes cm) below the beam's last key into the list; a full list is merged
-// first, and candidates that do not fit even then are merged directly
+// candidates ck (lanes cm, every one below the beam's last key: the caller has filtered
+// them against it) into the list; a full list is merged first, and candidates that do not
+// fit even then are merged directly
 template <int TR, int CR>
 __device__ __forceinline__ void pending_add(uint64_t (&beam)[TR], const uint64_t (&ck)[CR], const uint64_t (&cm)[CR],
                                             PendingList& pd, uint32_t T, uint64_t* scratch, uint64_t* aux,
                                             BeamState& st) {
-    uint64_t thr = readlane64(beam_reg<TR>(beam, (T - 1) >> 6), (T - 1) & 63u);
     uint64_t ok[CR];
     uint32_t n = 0;
 #pragma unroll
     for (int rc = 0; rc < CR; ++rc) {
-        ok[rc] = cm[rc] & ballot(ck[rc] < thr);
+        ok[rc] = cm[rc];
         n += static_cast<uint32_t>(__builtin_popcountll(ok[rc]));
     }
     if (n == 0) return;
     if (pd.n + n > 64u) {
         pending_flush<TR>(beam, pd, T, scratch, aux, st);
-        thr = readlane64(beam_reg<TR>(beam, (T - 1) >> 6), (T - 1) & 63u);
+        const uint64_t thr = readlane64(beam_reg<TR>(beam, (T - 1) >> 6), (T - 1) & 63u);
         n = 0;
 #pragma unroll
         for (int rc = 0; rc < CR; ++rc) {
@@ -503,7 +503,9 @@ __device__ __forceinline__ uint32_t pending_pick(uint64_t (&beam)[TR], BeamState
     uint64_t pmin = EMPTY_KEY;
     if (pd.n > 0) {
         const uint64_t um = (v & 1ull) ? EMPTY_KEY : v;
-        const uint64_t le = ballot(um <= ub && um != EMPTY_KEY);
+        // (when ub is EMPTY every lane qualifies and pmin is the plain minimum, EMPTY if the
+        // list holds no unmarked key)
+        const uint64_t le = ballot(um <= ub);
         if (le != 0)
             pmin = (le & (le - 1u)) == 0 ? readlane64(um, static_cast<uint32_t>(__builtin_ctzll(le))) : wave_min64(um);
     }
