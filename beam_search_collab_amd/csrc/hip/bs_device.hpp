@@ -426,7 +426,15 @@ struct PendingList {
     uint64_t* k;   // 64 key slots in the wave's LDS, the staging area of appends
     uint32_t n;    // keys held
     uint64_t v;    // the list itself: key `lane` in lane `lane` (< n), EMPTY_KEY above
+    uint64_t thr;  // the beam's last key (slot T - 1), kept current by the functions below,
+                   // the only ones that change the beam while the list is in use
 };
+
+// the beam's key in slot T - 1 (EMPTY_KEY while the beam is not full)
+template <int TR>
+__device__ __forceinline__ uint64_t beam_last(const uint64_t (&beam)[TR], uint32_t T) {
+    return readlane64(beam_reg<TR>(beam, (T - 1) >> 6), (T - 1) & 63u);
+}
 
 template <int TR>
 __device__ __forceinline__ void pending_flush(uint64_t (&beam)[TR], PendingList& pd, uint32_t T, uint64_t* scratch,
@@ -437,6 +445,7 @@ __device__ __forceinline__ void pending_flush(uint64_t (&beam)[TR], PendingList&
     beam_merge<TR, 1>(beam, ck, cm, T, scratch, aux, st);
     pd.n = 0;
     pd.v = EMPTY_KEY;
+    pd.thr = beam_last<TR>(beam, T);
 }
 
 // candidates ck (lanes cm, every one below the beam's last key: the caller has filtered
@@ -456,16 +465,16 @@ __device__ __forceinline__ void pending_add(uint64_t (&beam)[TR], const uint64_t
     if (n == 0) return;
     if (pd.n + n > 64u) {
         pending_flush<TR>(beam, pd, T, scratch, aux, st);
-        const uint64_t thr = readlane64(beam_reg<TR>(beam, (T - 1) >> 6), (T - 1) & 63u);
         n = 0;
 #pragma unroll
         for (int rc = 0; rc < CR; ++rc) {
-            ok[rc] &= ballot(ck[rc] < thr);
+            ok[rc] &= ballot(ck[rc] < pd.thr);
             n += static_cast<uint32_t>(__builtin_popcountll(ok[rc]));
         }
         if (n == 0) return;
         if (n > 64u) {
             beam_merge<TR, CR>(beam, ck, ok, T, scratch, aux, st);
+            pd.thr = beam_last<TR>(beam, T);
             return;
         }
     }
@@ -525,6 +534,7 @@ __device__ __forceinline__ uint32_t pending_pick(uint64_t (&beam)[TR], BeamState
             if (dup) {
                 pending_flush<TR>(beam, pd, T, scratch, aux, st);
                 const uint32_t id = beam_pick<TR, true>(beam, st);
+                pd.thr = beam_last<TR>(beam, T);  // the mark may have been slot T - 1's
                 picks += id != INVALID ? 1u : 0u;
                 return id;
             }
@@ -564,6 +574,7 @@ __device__ __forceinline__ uint32_t pending_pick(uint64_t (&beam)[TR], BeamState
     }
     const uint64_t lm = ml < 64u ? (1ull << ml) : 0ull;
     beam_mark<TR>(beam, mr, lm);
+    if (ml < 64u && 64u * mr + ml == T - 1u) pd.thr |= 1ull;
     return key_id(u);
 }
 

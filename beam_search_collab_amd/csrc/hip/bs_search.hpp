@@ -395,7 +395,8 @@ search_kernel(const SearchParams p) {
         constexpr bool DEFER = TR >= 8;
         // the list's append staging shares the merge scratch (live only between pending_add's
         // compaction and its read-back, when no merge runs)
-        PendingList pd = {DEFER ? reinterpret_cast<uint64_t*>(my + p.off_pend) : nullptr, 0u, EMPTY_KEY};
+        PendingList pd = {DEFER ? reinterpret_cast<uint64_t*>(my + p.off_pend) : nullptr, 0u, EMPTY_KEY,
+                          DEFER ? beam_last<TR>(beam, T) : EMPTY_KEY};
         uint32_t picks = 0;
         PhaseClock clk;
         clk.start();
@@ -486,7 +487,7 @@ search_kernel(const SearchParams p) {
             // neighbour's lookup; it is made only when per-query counters are requested.
             uint64_t ck[CR], cm[CR];
             uint32_t nv = 0;
-            const uint64_t thr_k = readlane64(beam_reg<TR>(beam, (T - 1) >> 6), (T - 1) & 63u);
+            const uint64_t thr_k = DEFER ? pd.thr : beam_last<TR>(beam, T);
             const bool count_all = p.per_query != nullptr;
 #pragma unroll
             for (int rc = 0; rc < CR; ++rc) {
