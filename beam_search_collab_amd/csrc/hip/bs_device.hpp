@@ -300,18 +300,18 @@ __device__ __forceinline__ void beam_merge(uint64_t (&beam)[TR], const uint64_t 
 // next_key (optional): the unexpanded key that follows the picked one in the beam
 // (EMPTY_KEY if none), for a prediction of the following pick.
 // beam_pick in two steps, for the deferred merge's pick (pending_pick): the beam's smallest
-// unexpanded key (EMPTY_KEY if none), not marked; `at` = its slot 64 r + l, st.first
-// advances to its register.
+// unexpanded key (EMPTY_KEY if none), not marked; `at` = its slot 64 r + l, `row_out` = the
+// register r itself, st.first advances to it.
 template <int TR>
 __device__ __forceinline__ uint64_t beam_peek(const uint64_t (&beam)[TR], BeamState& st, uint32_t& at,
-                                              uint64_t& row_mask) {
+                                              uint64_t& row_out) {
     uint32_t pr = st.first;
     uint64_t row, mp;
     for (;;) {
         if (pr >= static_cast<uint32_t>(TR)) {
             st.first = pr;
             at = 64u * TR;
-            row_mask = 0;
+            row_out = EMPTY_KEY;
             return EMPTY_KEY;
         }
         row = beam_reg<TR>(beam, pr);
@@ -322,7 +322,7 @@ __device__ __forceinline__ uint64_t beam_peek(const uint64_t (&beam)[TR], BeamSt
     st.first = pr;
     const uint32_t pl = static_cast<uint32_t>(__builtin_ctzll(mp));
     at = 64u * pr + pl;
-    row_mask = mp;
+    row_out = row;
     return readlane64(row, pl);
 }
 
@@ -504,8 +504,8 @@ __device__ __forceinline__ uint32_t pending_pick(uint64_t (&beam)[TR], BeamState
     const uint32_t lane = lane_id();
     const uint64_t v = pd.v;
     uint32_t at;
-    uint64_t mp;
-    const uint64_t ub = beam_peek<TR>(beam, st, at, mp);
+    uint64_t row;
+    const uint64_t ub = beam_peek<TR>(beam, st, at, row);
     // the list's smallest unmarked key, wanted only when it is <= ub: the lanes whose
     // unmarked key is <= ub say whether it is, and with one such lane the key is its key
     // (1M x 128, 10k queries, rabitq topk 512 3.72 -> 3.66 ms, 768 5.88 -> 5.84)
@@ -525,8 +525,10 @@ __device__ __forceinline__ uint32_t pending_pick(uint64_t (&beam)[TR], BeamState
     // (the beam's unmarked copies of u follow it)
     uint64_t kn = EMPTY_KEY;
     if (RUN && !from_list) {
+        // in the register beam_peek read unless u is its last lane
         const uint32_t nx = at + 1u;
-        if (nx < 64u * TR) kn = readlane64(beam_reg<TR>(beam, nx >> 6), nx & 63u);
+        if ((nx & 63u) != 0u) kn = readlane64(row, nx & 63u);
+        else if (nx < 64u * TR) kn = readlane64(beam_reg<TR>(beam, nx >> 6), 0u);
     }
     if constexpr (RUN) {
         if (pd.n > 0) {
