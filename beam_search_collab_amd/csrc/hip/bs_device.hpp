@@ -992,7 +992,8 @@ __host__ __device__ inline L2Shape l2_shape_lanes(uint32_t dim) {
 // row (l2_accum zeroes their difference) -- so all PB*QMAX loads of a lane are in flight
 // together (a conditional load would be followed by its own wait before the next one
 // issues).  rows[t] must point at a valid row for every lane (inactive groups pass row 0).
-template <int QMAX, int PB>
+// UNIFORM: every lane's rows[t] is the same (a picked node's record), loaded from a scalar base.
+template <int QMAX, int PB, bool UNIFORM = false>
 __device__ __forceinline__ void l2_load(const float* const (&rows)[PB], uint32_t lig, const L2Shape& L,
                                         float4 (&v)[PB][QMAX]) {
 #pragma unroll
@@ -1002,7 +1003,8 @@ __device__ __forceinline__ void l2_load(const float* const (&rows)[PB], uint32_t
         for (int kk = 0; kk < QMAX; ++kk) {
             const uint32_t j = lig + static_cast<uint32_t>(kk) * L.G;
             const bool ok = static_cast<uint32_t>(kk) < L.QR && j < L.chunks;
-            v[t][kk] = r4[ok ? j : 0u];
+            if constexpr (UNIFORM) v[t][kk] = bsw::load_off<float4>(r4, (ok ? j : 0u) << 4);
+            else v[t][kk] = r4[ok ? j : 0u];
         }
     }
 }
@@ -1264,11 +1266,11 @@ struct CodeHalves {
 __device__ __forceinline__ CodeHalves load_code_halves(const uint32_t* codes, uint32_t R, const QuadShape& S) {
     const uint32_t lane = lane_id();
     const uint32_t nb = lane & 31u, w = 2u * (lane >> 5);
+    // byte offsets from the record's codes, a wave-uniform base (bsw::load_off)
     CodeHalves h;
-    h.a = *reinterpret_cast<const uint2*>(codes + static_cast<uint64_t>(nb < R ? nb : 0u) * S.cws + w);
+    h.a = bsw::load_off<uint2>(codes, 4u * ((nb < R ? nb : 0u) * S.cws + w));
     h.b = make_uint2(0u, 0u);
-    if (R > 32u)
-        h.b = *reinterpret_cast<const uint2*>(codes + static_cast<uint64_t>(nb + 32u < R ? nb + 32u : 0u) * S.cws + w);
+    if (R > 32u) h.b = bsw::load_off<uint2>(codes, 4u * ((nb + 32u < R ? nb + 32u : 0u) * S.cws + w));
     return h;
 }
 

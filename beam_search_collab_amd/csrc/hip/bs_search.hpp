@@ -403,8 +403,11 @@ search_kernel(const SearchParams p) {
 
         for (int32_t iter = 0; iter < p.max_it; ++iter) {
             ++n_iter;
-            const uint32_t parent = DEFER ? pending_pick<TR, true>(beam, st, pd, T, scratch, merge_aux, picks)
-                                          : beam_pick<TR, true>(beam, st);
+            // the pick is wave-uniform; readfirstlane puts it in a scalar register (the
+            // compiler may leave it in a vector one), so that the record's addresses below
+            // are scalar bases with per-lane offsets
+            const uint32_t parent = uniform(DEFER ? pending_pick<TR, true>(beam, st, pd, T, scratch, merge_aux, picks)
+                                                  : beam_pick<TR, true>(beam, st));
             clk.mark(0);
             if (parent == INVALID) break;
             const uint32_t* rec = p.recs + static_cast<uint64_t>(parent) * rstride;
@@ -415,19 +418,21 @@ search_kernel(const SearchParams p) {
             // so an expansion costs one HBM round trip.  Indices are clamped, not masked.
             uint32_t child[CR];
             float ftx[CR], ffd[CR], ffv[CR];
+            // byte offsets from the record, a wave-uniform base (bsw::load_off; a record is a
+            // few KB)
 #pragma unroll
             for (int rc = 0; rc < CR; ++rc) {
                 const uint32_t i = static_cast<uint32_t>(rc) * 64u + lane;
                 const uint32_t ic = i < p.R ? i : 0u;
-                child[rc] = rec[p.rec_ids + ic];
-                ftx[rc] = fac[ic];
-                ffd[rc] = fac[p.R + ic];
-                ffv[rc] = fac[2 * p.R + ic];
+                child[rc] = bsw::load_off<uint32_t>(rec, 4u * (p.rec_ids + ic));
+                ftx[rc] = bsw::load_off<float>(fac, 4u * ic);
+                ffd[rc] = bsw::load_off<float>(fac, 4u * (p.R + ic));
+                ffv[rc] = bsw::load_off<float>(fac, 4u * (2u * p.R + ic));
             }
             float4 pv[1][QMAX];
             {
                 const float* const rows[1] = {reinterpret_cast<const float*>(rec)};
-                l2_load<QMAX, 1>(rows, lig, L, pv);
+                l2_load<QMAX, 1, true>(rows, lig, L, pv);
             }
             constexpr int NC = WIDE ? 4 : CR;
             uint4 cw[NC];

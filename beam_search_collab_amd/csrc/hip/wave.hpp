@@ -127,6 +127,17 @@ __device__ __forceinline__ float partner_f(float v) {
     return __uint_as_float(partner<S>(__float_as_uint(v)));
 }
 
+// Load of a T at byte offset `off` from a wave-uniform base (a record whose address the
+// wave computed from a picked node).  The empty asm (it emits nothing) keeps the compiler
+// from hoisting the offset's 64-bit extension out of the caller's loop, so the load takes
+// the base from scalar registers and the 32-bit offset from a vector register
+// (global_load ... voffset, saddr): no 64-bit address arithmetic per lane and load.
+template <typename T>
+__device__ __forceinline__ T load_off(const void* base, uint32_t off) {
+    asm volatile("" : "+v"(off));
+    return *reinterpret_cast<const T*>(static_cast<const char*>(base) + off);
+}
+
 // value of lane (this lane - 1); lane 0 gets lane 63's value
 __device__ __forceinline__ uint32_t prev_lane(uint32_t v) {
     return static_cast<uint32_t>(
