@@ -6,6 +6,9 @@
 //   xor 16        v_permlane16_swap + a select       (VALU)
 //   xor 32        v_permlane32_swap + a select       (VALU)
 //   shift by one  ds_bpermute
+// Butterfly reductions need less once the lanes of each group agree: one DPP mirror for the
+// partner quad or half-row, and the two results of one lane swap combined without a select
+// (partner, group_sum).
 #pragma once
 #include <hip/hip_runtime.h>
 #include <stdint.h>
